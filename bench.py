@@ -1,0 +1,316 @@
+#!/usr/bin/env python3
+"""Benchmark of the FlatQuant W4A4 hot path on one MI355X.
+
+Prints ONE JSON line. The primary workload (``value``) is BASELINE config 2:
+the fused quantize of fp16 X [2048, 4096] with 64 x 64 orthogonal transforms,
+clip 0.9, packed int32 codes — one "step" is one quantize call over that batch.
+``value`` is algorithmic HBM bytes (X in + codes out + fp32 scales + L, R) per
+second over exactly ``--steps`` back-to-back steps (a captured HIP graph,
+inputs already in HBM, rotated over enough buffers to exceed the 256 MB MALL),
+timed with HIP events on the stream the kernels run on.
+
+Secondary objects carry the W4A4 GEMM (config 4, TOPS vs the int8 MFMA peak),
+the wide quantize (config 3) and the end-to-end W4A4 linear (config 5).
+``cpu_baseline`` times this repo's CPU restatement of the reference PyTorch
+fallback on a bounded sample on the host cores (a reported baseline, not a target).
+
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-secondary] [--no-cpu]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, TOP/s
+MALL_BYTES = 256 * 2**20
+METRIC = "quantize GB/s + W4A4 GEMM TOPS on 1 MI355X; % of HBM / i8-MFMA roofline"
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _nbuf(bytes_per_set, minimum=2):
+    return max(minimum, math.ceil(1.25 * MALL_BYTES / max(1, bytes_per_set)))
+
+
+def _time_graph(torch, launch, steps, warmup):
+    """Warm up, capture ``steps`` launches in one graph, replay it once timed.
+
+    Returns (gpu_ms_total, wall_s_total). ``launch(i)`` issues step i on the
+    current stream.
+    """
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    g_warm = torch.cuda.CUDAGraph()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g_warm, stream=stream):
+            for i in range(max(1, warmup)):
+                launch(i)
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(steps):
+                launch(i)
+    torch.cuda.synchronize()
+    g_warm.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    t0 = time.perf_counter()
+    start.record(cur)
+    g.replay()
+    end.record(cur)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end), wall
+
+
+def bench_quant(torch, case, steps, warmup, dev):
+    from quant_ops_amd import capi
+
+    t, f = case.x.shape
+    per_set = case.algorithmic_bytes()
+    nbuf = _nbuf(per_set)
+    x0 = case.x.to(dev)
+    xs = [x0] + [x0.clone() for _ in range(nbuf - 1)]
+    L, R = case.left.to(dev), case.right.to(dev)
+    codes = [torch.empty((t, f // 8) if case.pack_int32 else (t, f),
+                         dtype=torch.int32 if case.pack_int32 else torch.int8, device=dev) for _ in range(nbuf)]
+    scales = [torch.empty(t, dtype=torch.float32, device=dev) for _ in range(nbuf)]
+
+    def launch(i):
+        j = i % nbuf
+        capi.flatquant_quantize(xs[j], L, R, case.clip_ratio, case.pack_int32, out_codes=codes[j],
+                                out_scales=scales[j])
+
+    gpu_ms, wall = _time_graph(torch, launch, steps, warmup)
+    per_step_s = gpu_ms / 1e3 / steps
+    gbs = per_set / per_step_s / 1e9
+    out = {
+        "workload": case.name, "tokens": t, "features": f, "M": case.left.shape[0], "N": case.right.shape[0],
+        "dtype": str(case.x.dtype).replace("torch.", ""), "clip_ratio": case.clip_ratio,
+        "pack_int32": case.pack_int32, "bytes_per_step": per_set, "flops_per_step": case.flops(),
+        "buffers_rotated": nbuf, "us_per_step": per_step_s * 1e6, "GBps": gbs,
+        "TFLOPs": case.flops() / per_step_s / 1e12, "wall_s": wall,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS},
+    }
+    del xs, codes, scales
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_gemm(torch, case, steps, warmup, dev):
+    from quant_ops_amd import capi
+
+    m, n, k = case.mnk
+    per_set = case.algorithmic_bytes()
+    nbuf = _nbuf(per_set)
+    a0, b0 = case.a.to(dev), case.b.to(dev)
+    As = [a0] + [a0.clone() for _ in range(nbuf - 1)]
+    Bs = [b0] + [b0.clone() for _ in range(nbuf - 1)] if b0.is_contiguous() else \
+        [b0] + [b0.t().clone().t() for _ in range(nbuf - 1)]
+    sa, sb = case.scale_a.to(dev), case.scale_b.to(dev)
+    outs = [torch.empty((m, n), dtype=case.out_dtype, device=dev) for _ in range(nbuf)]
+
+    def launch(i):
+        j = i % nbuf
+        capi.int4_gemm(As[j], Bs[j], sa, sb, out=outs[j])
+
+    gpu_ms, wall = _time_graph(torch, launch, steps, warmup)
+    per_step_s = gpu_ms / 1e3 / steps
+    tops = case.ops() / per_step_s / 1e12
+    out = {
+        "workload": case.name, "M": m, "N": n, "K": k, "b_layout": "KN" if b0.is_contiguous() else "W.t()",
+        "out_dtype": str(case.out_dtype).replace("torch.", ""), "ops_per_step": case.ops(),
+        "bytes_per_step": per_set, "buffers_rotated": nbuf, "us_per_step": per_step_s * 1e6, "TOPS": tops,
+        "GBps": per_set / per_step_s / 1e9, "wall_s": wall,
+        "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                     "frac": tops / INT8_PEAK_TOPS},
+    }
+    del As, Bs, outs
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_linear(torch, tokens, steps, warmup, dev):
+    """Config 5: bf16 X [T, 14336] -> quantize (112 x 128, clip 0.9) -> GEMM vs W.t() -> bf16 [T, 4096]."""
+    from quant_ops_amd import capi
+    from quant_ops_amd import workloads as wl
+
+    x = wl.activations(tokens, 14336, torch.bfloat16, seed=21, outlier_frac=0.005, outlier_scale=30.0).to(dev)
+    L, R = wl.orthogonal(112, 22, torch.bfloat16).to(dev), wl.orthogonal(128, 23, torch.bfloat16).to(dev)
+    w = wl.random_packed(4096, 1792, 24).to(dev)
+    sw = wl.uniform(4096, 0.001, 0.01, 25).to(dev)
+    codes = torch.empty(tokens, 1792, dtype=torch.int32, device=dev)
+    scales = torch.empty(tokens, dtype=torch.float32, device=dev)
+    out = torch.empty(tokens, 4096, dtype=torch.bfloat16, device=dev)
+
+    def launch(i):
+        capi.flatquant_quantize(x, L, R, 0.9, True, out_codes=codes, out_scales=scales)
+        capi.int4_gemm(codes, w.t(), scales, sw, out=out)
+
+    gpu_ms, wall = _time_graph(torch, launch, steps, warmup)
+    per_step_s = gpu_ms / 1e3 / steps
+    ops = 2 * tokens * 4096 * 14336
+    return {"workload": f"cfg5_w4a4_linear_down_proj_T{tokens}", "tokens": tokens,
+            "us_per_step": per_step_s * 1e6, "TOPS": ops / per_step_s / 1e12,
+            "weight_GBps": 4096 * 1792 * 4 / per_step_s / 1e9, "note": "quantize + GEMM, L2/MALL-warm inputs"}
+
+
+def cpu_baseline(torch, budget_s=12.0):
+    """The oracle (CPU restatement of the reference fallback) on config 2, bounded in time."""
+    from oracle import fq_reference as ofq
+    from quant_ops_amd import workloads as wl
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    case = wl.quant_cfg2()
+    ofq.flatquant_pytorch(case.x, case.left, case.right, case.clip_ratio, True)   # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        ofq.flatquant_pytorch(case.x, case.left, case.right, case.clip_ratio, True)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": case.algorithmic_bytes() / med / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"config 2 in full ([2048, 4096] fp16, packed), median of {len(times)} runs of the "
+                      f"oracle's torch-CPU fallback restatement ({med * 1e3:.1f} ms each); cpu: {cpu_model}; "
+                      f"torch {torch.__version__}"}
+
+
+def cpu_baseline_gemm(torch, budget_s=8.0):
+    """The oracle GEMM (unpack + float32 matmul + scales) on a 128-row slab of config 4."""
+    from oracle import int4_reference as oi4
+    from quant_ops_amd import workloads as wl
+
+    case = wl.gemm_case(128, 14336, 4096, seed=0)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {"value": case.ops() / med / 1e12, "unit": "TOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"128 x 14336 x 4096 slab of config 4, median of {len(times)} runs ({med:.2f} s each)"}
+
+
+def _traffic_from_profiles(kernel_key):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE), if committed."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as fh:
+            data = json.load(fh)
+        entry = data.get(kernel_key)
+        return None if entry is None else entry.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-secondary", action="store_true", help="only the primary workload")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (the hot path shards over tokens with no "
+              f"communication); --gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    sys.path.insert(0, ROOT)
+    import quant_ops_amd as qo
+    from quant_ops_amd import workloads as wl
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    if not qo.CUDA_AVAILABLE:
+        print(f"bench.py: HIP library not loaded: {qo._loader.LOAD_ERROR}", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+
+    _log("primary: config 2 quantize")
+    primary = bench_quant(torch, wl.quant_cfg2(), args.steps, args.warmup, dev)
+    primary["roofline"]["traffic"] = _traffic_from_profiles("quantize_cfg2")
+    _log(f"config 2: {primary['us_per_step']:.2f} us/step, {primary['GBps']:.0f} GB/s")
+
+    secondary = {}
+    if not args.no_secondary:
+        _log("secondary: config 4 GEMM")
+        secondary["gemm_cfg4"] = bench_gemm(torch, wl.gemm_cfg4(), args.steps, args.warmup, dev)
+        secondary["gemm_cfg4"]["roofline"]["traffic"] = _traffic_from_profiles("gemm_cfg4")
+        _log(f"config 4: {secondary['gemm_cfg4']['us_per_step']:.1f} us/step, "
+             f"{secondary['gemm_cfg4']['TOPS']:.0f} TOPS")
+        _log("secondary: config 3 quantize")
+        secondary["quantize_cfg3"] = bench_quant(torch, wl.quant_cfg3(), args.steps, args.warmup, dev)
+        _log(f"config 3: {secondary['quantize_cfg3']['us_per_step']:.1f} us/step, "
+             f"{secondary['quantize_cfg3']['GBps']:.0f} GB/s")
+        for t in (16, 4096):
+            _log(f"secondary: config 5 linear T={t}")
+            secondary[f"linear_cfg5_T{t}"] = bench_linear(torch, t, args.steps, args.warmup, dev)
+
+    cpu = None
+    if not args.no_cpu:
+        _log("cpu baseline (oracle on host cores)")
+        cpu = cpu_baseline(torch)
+        if not args.no_secondary:
+            secondary["gemm_cfg4"]["cpu_baseline"] = cpu_baseline_gemm(torch)
+
+    line = {
+        "metric": METRIC,
+        "value": primary["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": primary["us_per_step"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: seeded N(0,1) activations with 1% of channels x20, orthogonal transforms from QR "
+                "of seeded Gaussians",
+        "config": {
+            "workload": "BASELINE config 2: flatquant_dynamic_quantize fp16 X[2048,4096], M=N=64, "
+                        "clip_ratio=0.9, pack_int32=True (one step = one quantize call)",
+            "tokens": 2048, "features": 4096, "M": 64, "N": 64,
+        },
+        "roofline": primary["roofline"],
+        "cpu_baseline": cpu,
+        "primary": primary,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

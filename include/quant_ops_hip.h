@@ -1,0 +1,125 @@
+/*
+ * quant_ops_hip.h — C ABI of the MI355X (gfx950) FlatQuant W4A4 hot path.
+ *
+ * libquant_ops_hip.so exports these entry points. They take plain device
+ * pointers, sizes and strides (in elements), a dtype code and a HIP stream
+ * (as void*, NULL = the null stream). They never allocate, never synchronise
+ * the host, and return a status code (QO_OK = 0). Outputs are caller-owned.
+ *
+ * The reference binds the same work through pybind11 / TORCH_LIBRARY inside its
+ * CUDA translation units; each entry point names the reference function it
+ * replaces. The torch binding in quant_ops_amd/csrc/torch_ops.cpp registers
+ * the reference's operator schemas on top of these calls.
+ */
+#ifndef QUANT_OPS_HIP_H
+#define QUANT_OPS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types understood by the entry points. */
+enum qo_dtype {
+  QO_DTYPE_F32 = 0,
+  QO_DTYPE_F16 = 1,
+  QO_DTYPE_BF16 = 2,
+  QO_DTYPE_I8 = 3,
+  QO_DTYPE_I32 = 4
+};
+
+/* Status codes. The torch binding turns every non-zero code into a
+ * RuntimeError carrying qo_status_string(code) and the failing condition. */
+enum qo_status {
+  QO_OK = 0,
+  QO_ERR_NULL_POINTER = 1,  /* a required pointer is NULL */
+  QO_ERR_SHAPE = 2,         /* inconsistent or out-of-range sizes */
+  QO_ERR_DTYPE = 3,         /* dtype code not supported for that operand */
+  QO_ERR_ALIGNMENT = 4,     /* pointer / stride not aligned as required */
+  QO_ERR_UNSUPPORTED = 5,   /* valid request this build does not implement */
+  QO_ERR_LAUNCH = 6         /* hipLaunchKernel (or hipGetLastError) failed */
+};
+
+/* Human-readable name of a status code (static storage). */
+const char* qo_status_string(int status);
+
+/* Library version string, e.g. "0.1.0". */
+const char* qo_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* qo_last_error(void);
+
+/*
+ * Fused FlatQuant dynamic int4 quantization, one pass over X.
+ *
+ * Replaces cuda_kronecker_quant_int8 (flatquant/kernels/cuda_quant_kernel.cu:316-390),
+ * the CUDA implementation behind quant_ops::flatquant_dynamic_quantize
+ * (cuda_quant_kernel.cu:395-413). For every token t (row of X, viewed as an
+ * M x N matrix, feature f = m*N + n) it computes Y = L^T (X R) with the
+ * rounding points of the reference's PyTorch fallback (flatquant/ops.py:99-117),
+ * the per-token scale s = max(|rnd(min Y * c)|, rnd(max Y * c)) / 7 (floored at
+ * rnd(1e-8)), and codes clamp(round_half_even(rnd(Y / s)), -8, 7).
+ *
+ *   x           [tokens, M*N] of x_dtype (F32, F16 or BF16), row stride x_ld
+ *               elements, unit inner stride
+ *   left, right [M, M] and [N, N] row-major, same dtype as x
+ *   clip_ratio  the reference's clip_ratio (applied as a float32 product)
+ *   pack_int32  0: out_codes is int8 [tokens, M*N] (row stride M*N)
+ *               1: out_codes is int32 [tokens, M*N/8]; word p holds features
+ *                  8p..8p+7, code i in bits 4i..4i+3 as (q + 8)
+ *   out_scales  float32 [tokens]: the scale rounded to x_dtype, as float32
+ *
+ * Errors: QO_ERR_SHAPE if M*N % 8 != 0 while pack_int32, tokens < 0, M or N < 1;
+ * QO_ERR_DTYPE for other x_dtype codes.
+ */
+int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
+                          const void* left, const void* right, int M, int N,
+                          float clip_ratio, int pack_int32,
+                          void* out_codes, float* out_scales, void* stream);
+
+/*
+ * W4A4 GEMM: out[m, n] = rnd_out((float(acc[m, n]) * scale_a[m]) * scale_b[n]),
+ * acc[m, n] = sum_k qa[m, k] * qb[k, n] exactly in int32.
+ *
+ * Replaces cuda_int4_matmul (int4_matmul/kernels/cuda_int4_matmul_kernel.cu:130-189),
+ * the CUDA implementation behind quant_ops::int4_matmul
+ * (cuda_int4_matmul_kernel.cu:194-214); numerics follow the fallback
+ * int4_matmul_pytorch (int4_matmul/ops.py:69-103).
+ *
+ *   a        int32 [M, K/8], word (m, p) holds k = 8p..8p+7; row stride lda words
+ *   b        int32 words, word (p, n) holds k = 8p..8p+7 of column n, located at
+ *            b[p * b_stride_p + n * b_stride_n]. Either stride may be 1:
+ *            b_stride_n == 1 is the reference's row-major [K/8, N] tensor,
+ *            b_stride_p == 1 is the transposed view W.t() of a [N, K/8] weight.
+ *   scale_a  [M] of scale_a_dtype (F32, F16, BF16)
+ *   scale_b  [N] of scale_b_dtype (F32, F16, BF16)
+ *   out      [M, N] of out_dtype (F16 as the reference, or BF16 / F32), row stride ldc
+ *   K        multiple of 8, K < 2^21
+ */
+int qo_int4_gemm(const int32_t* a, int64_t lda,
+                 const int32_t* b, int64_t b_stride_p, int64_t b_stride_n,
+                 const void* scale_a, int scale_a_dtype,
+                 const void* scale_b, int scale_b_dtype,
+                 void* out, int out_dtype, int64_t ldc,
+                 int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * Dequantize int4 codes: out[t, f] = float(q[t, f]) * float(scales[t]) (float32).
+ *
+ * Replaces dequantize_int4 (flatquant/ops.py:156-178), which the reference runs
+ * as torch element-wise operations.
+ *
+ *   codes        int8 [tokens, features] (pack_int32 = 0) or int32
+ *                [tokens, features/8] (pack_int32 = 1), contiguous rows
+ *   scales       [tokens] of scale_dtype (F32, F16, BF16)
+ *   out          float32 [tokens, features], contiguous
+ */
+int qo_dequantize_int4(const void* codes, int pack_int32, const void* scales, int scale_dtype,
+                       int64_t tokens, int64_t features, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUANT_OPS_HIP_H */

@@ -1,0 +1,124 @@
+"""ctypes binding of the C ABI in ``include/quant_ops_hip.h``.
+
+This is the FFI view of ``libquant_ops_hip.so``: plain device pointers, sizes,
+strides and a stream handle, no torch types. Tests and the benchmark call the
+kernels through it; torch tensors are only used here to own device memory and
+to name the current stream. Every call raises ``QuantOpsError`` on a non-zero
+status, with the library's message.
+"""
+import ctypes
+import os
+
+import torch
+
+from ._loader import HIP_LIB_PATH
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_I8, DTYPE_I32 = 0, 1, 2, 3, 4
+STATUS = {0: "QO_OK", 1: "QO_ERR_NULL_POINTER", 2: "QO_ERR_SHAPE", 3: "QO_ERR_DTYPE",
+          4: "QO_ERR_ALIGNMENT", 5: "QO_ERR_UNSUPPORTED", 6: "QO_ERR_LAUNCH"}
+
+# Every symbol the header declares; the CPU tests check they are all exported.
+EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_flatquant_quantize",
+            "qo_int4_gemm", "qo_dequantize_int4")
+
+_TORCH_CODE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+
+
+class QuantOpsError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+_lib = None
+
+
+def lib():
+    """Load (once) and return the ctypes handle with argument types set."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(HIP_LIB_PATH):
+        raise QuantOpsError(5, f"{HIP_LIB_PATH} is not built")
+    L = ctypes.CDLL(HIP_LIB_PATH)
+    c_i64, c_int, c_vp, c_f = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float
+    L.qo_status_string.restype = ctypes.c_char_p
+    L.qo_status_string.argtypes = [c_int]
+    L.qo_version.restype = ctypes.c_char_p
+    L.qo_version.argtypes = []
+    L.qo_last_error.restype = ctypes.c_char_p
+    L.qo_last_error.argtypes = []
+    L.qo_flatquant_quantize.restype = c_int
+    L.qo_flatquant_quantize.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_int,
+                                        c_vp, c_vp, c_vp]
+    L.qo_int4_gemm.restype = c_int
+    L.qo_int4_gemm.argtypes = [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_int, c_vp, c_int, c_vp, c_int, c_i64,
+                               c_i64, c_i64, c_i64, c_vp]
+    L.qo_dequantize_int4.restype = c_int
+    L.qo_dequantize_int4.argtypes = [c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_vp, c_vp]
+    _lib = L
+    return L
+
+
+def _check(status):
+    if status != 0:
+        raise QuantOpsError(status, lib().qo_last_error().decode())
+
+
+def _stream(stream):
+    if stream is None:
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, torch.cuda.Stream):
+        return ctypes.c_void_p(stream.cuda_stream)
+    return ctypes.c_void_p(stream)
+
+
+def version() -> str:
+    return lib().qo_version().decode()
+
+
+def flatquant_quantize(x, left, right, clip_ratio=1.0, pack_int32=False, out_codes=None, out_scales=None,
+                       stream=None):
+    """Call ``qo_flatquant_quantize`` on device tensors; allocates outputs if not given."""
+    t, f = x.shape
+    m, n = left.shape[0], right.shape[0]
+    if out_codes is None:
+        out_codes = torch.empty((t, f // 8) if pack_int32 else (t, f),
+                                dtype=torch.int32 if pack_int32 else torch.int8, device=x.device)
+    if out_scales is None:
+        out_scales = torch.empty((t,), dtype=torch.float32, device=x.device)
+    _check(lib().qo_flatquant_quantize(
+        ctypes.c_void_p(x.data_ptr()), _TORCH_CODE[x.dtype], t, x.stride(0) if t else f,
+        ctypes.c_void_p(left.data_ptr()), ctypes.c_void_p(right.data_ptr()), m, n,
+        float(clip_ratio), 1 if pack_int32 else 0,
+        ctypes.c_void_p(out_codes.data_ptr()), ctypes.c_void_p(out_scales.data_ptr()), _stream(stream)))
+    return out_codes, out_scales
+
+
+def int4_gemm(a, b, scale_a, scale_b, out_dtype=torch.float16, out=None, stream=None):
+    """Call ``qo_int4_gemm``; ``b`` may be row-major [K/8, N] or the ``W.t()`` view."""
+    m, kp = a.shape
+    n = b.shape[1]
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=a.device)
+    _check(lib().qo_int4_gemm(
+        ctypes.c_void_p(a.data_ptr()), a.stride(0) if m else kp,
+        ctypes.c_void_p(b.data_ptr()), b.stride(0), b.stride(1),
+        ctypes.c_void_p(scale_a.data_ptr()), _TORCH_CODE[scale_a.dtype],
+        ctypes.c_void_p(scale_b.data_ptr()), _TORCH_CODE[scale_b.dtype],
+        ctypes.c_void_p(out.data_ptr()), _TORCH_CODE[out.dtype], out.stride(0) if m else n,
+        m, n, kp * 8, _stream(stream)))
+    return out
+
+
+def dequantize_int4(codes, scales, packed_int32=False, out=None, stream=None):
+    """Call ``qo_dequantize_int4``; returns float32 [T, F]."""
+    t = codes.shape[0]
+    f = codes.shape[1] * (8 if packed_int32 else 1)
+    if out is None:
+        out = torch.empty((t, f), dtype=torch.float32, device=codes.device)
+    _check(lib().qo_dequantize_int4(
+        ctypes.c_void_p(codes.data_ptr()), 1 if packed_int32 else 0,
+        ctypes.c_void_p(scales.data_ptr()), _TORCH_CODE[scales.dtype], t, f,
+        ctypes.c_void_p(out.data_ptr()), _stream(stream)))
+    return out

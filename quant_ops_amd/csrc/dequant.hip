@@ -1,0 +1,89 @@
+// Dequantize int4 codes to float32: out[t, f] = float(q[t, f]) * float(scale[t]).
+//
+// Replaces dequantize_int4 (flatquant/ops.py:156-178), which the reference runs
+// as eight strided torch passes for the packed layout. HBM-bound: each thread
+// reads one packed word (or 8 int8 codes) and writes 32 bytes of float32.
+#include "common.h"
+
+namespace qo {
+
+template <bool PACKED>
+__global__ void __launch_bounds__(256)
+dequant_kernel(const void* __restrict__ codes, const void* __restrict__ scales, int sd, int64_t tokens,
+               int64_t words_per_row, float* __restrict__ out) {
+  const int64_t total = tokens * words_per_row;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t t = i / words_per_row;
+    const float s = load_scale(scales, sd, t);
+    float v[8];
+    if (PACKED) {
+      const uint32_t w = (uint32_t)reinterpret_cast<const int32_t*>(codes)[i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (float)((int)((w >> (4 * j)) & 0xF) - 8) * s;
+    } else {
+      const v2i c = reinterpret_cast<const v2i*>(codes)[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = (float)(int8_t)((uint32_t)c[0] >> (8 * j)) * s;
+        v[4 + j] = (float)(int8_t)((uint32_t)c[1] >> (8 * j)) * s;
+      }
+    }
+    v4f* o = reinterpret_cast<v4f*>(out + i * 8);
+    o[0] = v4f{v[0], v[1], v[2], v[3]};
+    o[1] = v4f{v[4], v[5], v[6], v[7]};
+  }
+}
+
+// Tail-safe variant for features % 8 != 0 (int8 codes only).
+__global__ void __launch_bounds__(256)
+dequant_i8_any(const int8_t* __restrict__ codes, const void* __restrict__ scales, int sd, int64_t tokens,
+               int64_t features, float* __restrict__ out) {
+  const int64_t total = tokens * features;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256)
+    out[i] = (float)codes[i] * load_scale(scales, sd, i / features);
+}
+
+}  // namespace qo
+
+extern "C" int qo_dequantize_int4(const void* codes, int pack_int32, const void* scales, int scale_dtype,
+                                  int64_t tokens, int64_t features, float* out, void* stream) {
+  using namespace qo;
+  if (tokens < 0 || features < 0 || (pack_int32 && features % 8 != 0)) {
+    qo_set_error("qo_dequantize_int4: invalid sizes tokens=%lld features=%lld", (long long)tokens,
+                 (long long)features);
+    return QO_ERR_SHAPE;
+  }
+  if (scale_dtype != QO_DTYPE_F32 && scale_dtype != QO_DTYPE_F16 && scale_dtype != QO_DTYPE_BF16) {
+    qo_set_error("qo_dequantize_int4: unsupported scale dtype code %d", scale_dtype);
+    return QO_ERR_DTYPE;
+  }
+  if (tokens == 0 || features == 0) return QO_OK;
+  if (!codes || !scales || !out) {
+    qo_set_error("qo_dequantize_int4: NULL pointer argument");
+    return QO_ERR_NULL_POINTER;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = (features % 8 == 0) && ((uintptr_t)out % 16 == 0) && (pack_int32 || (uintptr_t)codes % 8 == 0);
+  if (vec) {
+    const int64_t wpr = features / 8;
+    int64_t blocks = (tokens * wpr + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (pack_int32)
+      hipLaunchKernelGGL(dequant_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, codes, scales, scale_dtype,
+                         tokens, wpr, out);
+    else
+      hipLaunchKernelGGL(dequant_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, codes, scales,
+                         scale_dtype, tokens, wpr, out);
+  } else {
+    int64_t blocks = (tokens * features + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(dequant_i8_any, dim3((unsigned)blocks), dim3(256), 0, s,
+                       reinterpret_cast<const int8_t*>(codes), scales, scale_dtype, tokens, features, out);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    qo_set_error("qo_dequantize_int4: launch failed: %s", hipGetErrorString(e));
+    return QO_ERR_LAUNCH;
+  }
+  return QO_OK;
+}

@@ -1,0 +1,561 @@
+// Fused FlatQuant dynamic int4 quantization for gfx950 (MI355X).
+//
+// One pass over X per token: Y = rnd_D(L^T rnd_D(X R)), per-token absmax scale,
+// round-half-even codes clamped to [-8, 7], optional 8-nibble int32 packing.
+// Replaces the reference's cuBLAS + scale_quant_kernel chain
+// (flatquant/kernels/cuda_quant_kernel.cu:231-390) and follows the rounding
+// points of its PyTorch fallback (flatquant/ops.py:99-130).
+//
+// Two kernels:
+//  * fq_mfma_kernel   — D in {fp16, bf16}, M % 16 == 0 (M <= 128), N in {32, 64, 128}.
+//                       Both contractions on v_mfma_f32_16x16x32_{f16,bf16}; X is
+//                       streamed into LDS by LDS-DMA (global_load_lds_dwordx4)
+//                       one token group ahead; L is resident in LDS, R in VGPRs.
+//  * fq_generic_kernel — any M, N, D in {fp32, fp16, bf16}; VALU fp32 FMA with the
+//                       same rounding points. Used for shapes the MFMA kernel
+//                       does not cover (and for fp32 inputs).
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+
+namespace qo {
+
+// ---------------------------------------------------------------------------
+// Scale and code, shared by both kernels.
+// ---------------------------------------------------------------------------
+
+// Per-token scale from the raw (unrounded) fp32 extremes of Y. Rounding to D is
+// monotonic, so rnd_D(max y) == max rnd_D(y): this is amax/amin of the D tensor
+// (ops.py:108-109), then maximum(|rnd(min*c)|, rnd(max*c)) (ops.py:112), then
+// rnd(./7) clamped below by rnd_D(1e-8) (ops.py:113).
+template <class DT>
+__device__ inline float fq_scale(float ymax_raw, float ymin_raw, float clip) {
+  const float hi = DT::round(ymax_raw);
+  const float lo = DT::round(ymin_raw);
+  const float t_lo = DT::round(lo * clip);
+  const float t_hi = DT::round(hi * clip);
+  const float bound = fmaxf(fabsf(t_lo), t_hi);
+  const float s = DT::round(bound / 7.0f);
+  return fmaxf(s, DT::round(1e-8f));
+}
+
+// Code of one element from its D-rounded quotient t = rnd_D(y / s):
+// clamp(round_half_even(t), -8, 7) (ops.py:117). A NaN quotient (0/0 when an
+// fp16 token's scale rounds to 0) becomes 0 through the reference's int8 cast
+// and nibble 0 (code -8) through its uint8 cast before packing (ops.py:122);
+// both are reproduced here.
+template <bool PACK>
+__device__ inline int fq_code_from_quot(float t) {
+  if (t != t) return PACK ? -8 : 0;
+  const float c = fminf(fmaxf(t, -8.0f), 7.0f);
+  return (int)__builtin_rintf(c);
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernel: one 256-thread block per token (grid-stride over tokens).
+// LDS holds X (as D) and Z (as D); Y overwrites X.
+// ---------------------------------------------------------------------------
+template <class DT, bool PACK>
+__global__ void __launch_bounds__(256)
+fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+                  const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right,
+                  int M, int N, float clip, void* __restrict__ out_codes,
+                  float* __restrict__ out_scales) {
+  using T = typename DT::T;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int F = M * N;
+  T* xs = reinterpret_cast<T*>(smem);
+  T* zs = xs + F;
+  __shared__ float red_hi[4], red_lo[4], s_scale;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
+    const T* xt = x + t * x_ld;
+    for (int f = tid; f < F; f += 256) xs[f] = xt[f];
+    __syncthreads();
+    // Z = rnd_D(X R): Z[m][n] = sum_k X[m][k] R[k][n]
+    for (int f = tid; f < F; f += 256) {
+      const int m = f / N, n = f - m * N;
+      float acc = 0.f;
+      for (int k = 0; k < N; ++k) acc = fmaf(DT::to_f(xs[m * N + k]), DT::to_f(right[k * N + n]), acc);
+      zs[f] = DT::from_f(acc);
+    }
+    __syncthreads();
+    // Y = rnd_D(L^T Z): Y[m][n] = sum_k L[k][m] Z[k][n]
+    float hi = -INFINITY, lo = INFINITY;
+    for (int f = tid; f < F; f += 256) {
+      const int m = f / N, n = f - m * N;
+      float acc = 0.f;
+      for (int k = 0; k < M; ++k) acc = fmaf(DT::to_f(left[k * M + m]), DT::to_f(zs[k * N + n]), acc);
+      const T y = DT::from_f(acc);
+      xs[f] = y;
+      hi = fmaxf(hi, DT::to_f(y));
+      lo = fminf(lo, DT::to_f(y));
+    }
+    hi = wave_max(hi);
+    lo = wave_min(lo);
+    if (lane == 0) { red_hi[wave] = hi; red_lo[wave] = lo; }
+    __syncthreads();
+    if (tid == 0) {
+      float h = red_hi[0], l = red_lo[0];
+      for (int w = 1; w < 4; ++w) { h = fmaxf(h, red_hi[w]); l = fminf(l, red_lo[w]); }
+      const float s = fq_scale<DT>(h, l, clip);
+      s_scale = s;
+      out_scales[t] = s;
+    }
+    __syncthreads();
+    const float s = s_scale;
+    if (PACK) {
+      int32_t* o = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8);
+      for (int p = tid; p < F / 8; p += 256) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float q = DT::round(DT::to_f(xs[8 * p + i]) / s);
+          word |= (uint32_t)(fq_code_from_quot<true>(q) + 8) << (4 * i);
+        }
+        o[p] = (int32_t)word;
+      }
+    } else {
+      int8_t* o = reinterpret_cast<int8_t*>(out_codes) + t * F;
+      for (int f = tid; f < F; f += 256) {
+        const float q = DT::round(DT::to_f(xs[f]) / s);
+        o[f] = (int8_t)fq_code_from_quot<false>(q);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA kernel.
+//
+// Shapes: M = 16*MB, N = 32*NP. A "pair" q is the 32 columns n in [32q, 32q+32),
+// i.e. output words 4q..4q+3 of each row m. Each wave owns one (token, pair);
+// NP waves share a token, TPB = WAVES/NP tokens are in flight per block.
+//
+// Column permutation: inside pair q, MFMA block h (0/1) lane-column i (0..15)
+// is physical column n = 32q + 8*(i/4) + 4h + (i%4). With that choice the
+// second product, computed transposed (Y^T = Z^T L with Z's accumulator
+// fragment reused as the A operand), leaves lane (g = lane/16) holding
+// Y[m][32q + 8g + 0..7] — the eight features of one packed word — so packing
+// needs no cross-lane traffic.
+//
+// MFMA 16x16x32 operand convention used throughout: lane l supplies row/column
+// l%16 and the eight k values 8*(l/16) + 0..7 of the current 32-deep slab; the
+// accumulator holds rows 4*(l/16) + r, r = 0..3, of column l%16. The k order
+// only has to agree between the A and B operands.
+// ---------------------------------------------------------------------------
+
+template <class DT>
+struct MfmaOps;
+
+template <>
+struct MfmaOps<F16T> {
+  using V = v8h;
+  __device__ static inline v4f mfma(V a, V b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct MfmaOps<BF16T> {
+  using V = v8bf;
+  __device__ static inline v4f mfma(V a, V b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <int MB, int NP>
+struct FqShape {
+  static constexpr int M = 16 * MB;
+  static constexpr int N = 32 * NP;
+  static constexpr int F = M * N;
+  static constexpr int KS1 = NP;             // 32-deep slabs of the first product (k = n')
+  static constexpr int KS2 = (MB + 1) / 2;   // 32-deep slabs of the second product (k = m')
+  static constexpr int XFRAGS = MB * KS1;    // 1 KiB A fragments per token
+  // 8 waves unless the X double buffer + L would not fit in 160 KiB of LDS.
+  static constexpr int WAVES = (16 * MB + MB * KS2 <= 150) ? 8 : 4;
+  static constexpr int TPB = WAVES / NP;     // tokens per block iteration
+  static constexpr int STAGE_FRAGS = TPB * XFRAGS;
+  static constexpr int DMA_PER_WAVE = STAGE_FRAGS / WAVES;
+  static constexpr int LFRAGS = MB * KS2;
+  static_assert(WAVES % NP == 0, "waves per block must be a multiple of pairs per token");
+  static_assert(STAGE_FRAGS % WAVES == 0, "X fragments must split evenly over waves");
+};
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+// vmcnt is 6 bits on gfx9 (0..63); the encoding keeps lgkmcnt / expcnt at max.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barriers without the release/acquire fences of __syncthreads():
+// those fences wait for every outstanding vector-memory operation (vmcnt(0)),
+// which would also wait for the next group's X prefetch. The "memory" clobber
+// keeps the compiler from moving memory accesses across the barrier.
+__device__ inline void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One token group (this wave's token slot and pair) from an X stage in LDS:
+// both products, the per-token scale and the codes.
+template <class DT, int MB, int NP, bool PACK>
+__device__ __attribute__((always_inline)) inline void fq_mfma_group(
+    const typename DT::T* __restrict__ xs, const typename DT::T* __restrict__ lfrag,
+    const typename MfmaOps<DT>::V (&rf)[2][FqShape<MB, NP>::KS1], float (*red)[NP][2], int64_t t,
+    int64_t tokens, float clip, void* __restrict__ out_codes, float* __restrict__ out_scales, int lane,
+    int tau, int q) {
+  using S = FqShape<MB, NP>;
+  using T = typename DT::T;
+  using Ops = MfmaOps<DT>;
+  using V = typename Ops::V;
+  constexpr int N = S::N, F = S::F, KS1 = S::KS1, KS2 = S::KS2;
+  const int li = lane & 15, lg = lane >> 4;
+
+  // First product, one 16-row block of Z at a time: Z[rb] = X[rb] R[:, pair].
+  V zp[2][KS2];
+#pragma unroll
+  for (int rb = 0; rb < MB; ++rb) {
+    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks) {
+      const V a = *reinterpret_cast<const V*>(xs + ((rb * KS1 + ks) * 64 + lane) * 8);
+      acc0 = Ops::mfma(a, rf[0][ks], acc0);
+      acc1 = Ops::mfma(a, rf[1][ks], acc1);
+    }
+    // Rounding point 1, and the accumulator -> A-operand hand-off.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      zp[0][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc0[r]);
+      zp[1][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc1[r]);
+    }
+  }
+  if (MB & 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      zp[0][KS2 - 1][4 + r] = DT::from_f(0.f);
+      zp[1][KS2 - 1][4 + r] = DT::from_f(0.f);
+    }
+  }
+
+  // Second product, transposed: Y^T[n][m] = sum_m' Z[m'][n] L[m'][m].
+  float yv[MB][8];
+  float hi = -INFINITY, lo = INFINITY;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS2; ++s) {
+      const V b = *reinterpret_cast<const V*>(lfrag + ((mb * KS2 + s) * 64 + lane) * 8);
+      acc0 = Ops::mfma(zp[0][s], b, acc0);
+      acc1 = Ops::mfma(zp[1][s], b, acc1);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      hi = fmaxf(hi, fmaxf(acc0[r], acc1[r]));
+      lo = fminf(lo, fminf(acc0[r], acc1[r]));
+      yv[mb][r] = DT::round(acc0[r]);  // rounding point 2
+      yv[mb][4 + r] = DT::round(acc1[r]);
+    }
+  }
+
+  hi = wave_max(hi);
+  lo = wave_min(lo);
+  if (lane == 0) {
+    red[tau][q][0] = hi;
+    red[tau][q][1] = lo;
+  }
+  lds_barrier();
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    hi = fmaxf(hi, red[tau][p][0]);
+    lo = fminf(lo, red[tau][p][1]);
+  }
+  const float s = fq_scale<DT>(hi, lo, clip);
+  if (t >= tokens) return;
+  if (q == 0 && lane == 0) out_scales[t] = s;
+  const float rcp = 1.0f / s;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = 16 * mb + li;
+    int code[8];
+    if (s > 0.f) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float tq = DT::round(yv[mb][j] * rcp);
+        code[j] = (int)__builtin_rintf(fminf(fmaxf(tq, -8.0f), 7.0f));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) code[j] = fq_code_from_quot<PACK>(DT::round(yv[mb][j] / s));
+    }
+    if (PACK) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) word |= (uint32_t)(code[j] + 8) << (4 * j);
+      reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (N / 8) + 4 * q + lg] = (int32_t)word;
+    } else {
+      uint32_t lo4 = 0, hi4 = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo4 |= (uint32_t)(code[j] & 0xFF) << (8 * j);
+        hi4 |= (uint32_t)(code[4 + j] & 0xFF) << (8 * j);
+      }
+      v2i pair = {(int)lo4, (int)hi4};
+      *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + m * N + 32 * q + 8 * lg) = pair;
+    }
+  }
+}
+
+template <class DT, int MB, int NP, bool PACK>
+__global__ void __launch_bounds__((FqShape<MB, NP>::WAVES * 64))
+fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+               const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right,
+               float clip, void* __restrict__ out_codes, float* __restrict__ out_scales) {
+  using S = FqShape<MB, NP>;
+  using T = typename DT::T;
+  using V = typename MfmaOps<DT>::V;
+  constexpr int M = S::M, N = S::N, KS1 = S::KS1, KS2 = S::KS2;
+
+  // Two X stages as distinct objects: the compiler then knows that reading one
+  // stage does not depend on the LDS-DMA still writing the other.
+  __shared__ __align__(16) T lfrag[S::LFRAGS * 64 * 8];
+  __shared__ __align__(16) T xbuf0[S::STAGE_FRAGS * 64 * 8];
+  __shared__ __align__(16) T xbuf1[S::STAGE_FRAGS * 64 * 8];
+  __shared__ float red[S::TPB][NP][2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int tau = wave / NP;   // token slot of this wave
+  const int q = wave % NP;     // column pair of this wave
+  const int li = lane & 15;    // lane row / column inside a 16x16 block
+  const int lg = lane >> 4;    // lane group: k values 8*lg .. 8*lg+7
+
+  // L as B-operand fragments of the second product: fragment (mb, s), lane l,
+  // element j holds L[m'][m], m = 16mb + l%16, m' = 32s + 16(j/4) + 4(l/16) + j%4
+  // (zero for m' >= M). This m' order is the row order of Z's accumulator pairs.
+  for (int e = tid; e < S::LFRAGS * 64 * 8; e += S::WAVES * 64) {
+    const int j = e & 7, l = (e >> 3) & 63, fr = e >> 9;
+    const int mb = fr / KS2, s = fr % KS2;
+    const int m = 16 * mb + (l & 15);
+    const int mp = 32 * s + 16 * (j >> 2) + 4 * (l >> 4) + (j & 3);
+    lfrag[e] = (mp < M) ? left[mp * M + m] : DT::from_f(0.f);
+  }
+
+  // R as B-operand fragments of the first product for this wave's pair:
+  // rf[h][ks][j] = R[32ks + 8lg + j][n], n = 32q + 8(li/4) + 4h + li%4.
+  V rf[2][KS1];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int n = 32 * q + 8 * (li >> 2) + 4 * h + (li & 3);
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rf[h][ks][j] = right[(32 * ks + 8 * lg + j) * N + n];
+  }
+
+  // LDS-DMA of one token group into a stage. Fragment c of the stage is token
+  // slot c / XFRAGS, block (rb, ks); lane l fetches X[16rb + l%16][32ks + 8(l/16) .. +7]
+  // (16 bytes), which the hardware writes to fragment base + 16*l.
+  const int64_t ngroups = (tokens + S::TPB - 1) / S::TPB;
+  auto issue = [&](int64_t g, T* stage) {
+#pragma unroll
+    for (int i = 0; i < S::DMA_PER_WAVE; ++i) {
+      const int c = wave + i * S::WAVES;
+      const int ts = c / S::XFRAGS, fr = c % S::XFRAGS;
+      const int rb = fr / KS1, ks = fr % KS1;
+      int64_t t = g * S::TPB + ts;
+      t = t < tokens ? t : tokens - 1;  // tail slots re-read a valid row; never stored
+      const T* src = x + t * x_ld + (16 * rb + li) * N + 32 * ks + 8 * lg;
+      __builtin_amdgcn_global_load_lds((const void*)src,
+                                       (__attribute__((address_space(3))) void*)(stage + c * 512), 16, 0, 0);
+    }
+  };
+  // Before reading a stage: issue the next group into the other stage (past
+  // the last group the DMA re-reads the last token, so every iteration issues
+  // the same number of loads), wait for this wave's DMA of the current group
+  // (loads complete in order, so at most DMA_PER_WAVE outstanding means the
+  // older group has landed), then a barrier so every wave's part is visible.
+  auto prefetch_and_wait = [&](int64_t gn, T* other) {
+    issue(gn < ngroups ? gn : ngroups - 1, other);
+    wait_vmcnt<S::DMA_PER_WAVE>();
+    raw_barrier();
+  };
+
+  int64_t g = blockIdx.x;
+  if (g < ngroups) issue(g, xbuf0);
+  lds_barrier();  // lfrag visible
+
+  while (g < ngroups) {
+    int64_t gn = g + gridDim.x;
+    prefetch_and_wait(gn, xbuf1);
+    fq_mfma_group<DT, MB, NP, PACK>(xbuf0 + tau * S::XFRAGS * 512, lfrag, rf, red, g * S::TPB + tau, tokens,
+                                    clip, out_codes, out_scales, lane, tau, q);
+    g = gn;
+    if (g >= ngroups) break;
+    gn = g + gridDim.x;
+    prefetch_and_wait(gn, xbuf0);
+    fq_mfma_group<DT, MB, NP, PACK>(xbuf1 + tau * S::XFRAGS * 512, lfrag, rf, red, g * S::TPB + tau, tokens,
+                                    clip, out_codes, out_scales, lane, tau, q);
+    g = gn;
+  }
+  wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
+}
+
+// ---------------------------------------------------------------------------
+// Host-side dispatch.
+// ---------------------------------------------------------------------------
+
+static int device_cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+template <class DT, int MB, int NP, bool PACK>
+static int launch_mfma(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right,
+                       float clip, void* out_codes, float* out_scales, hipStream_t stream) {
+  using S = FqShape<MB, NP>;
+  using T = typename DT::T;
+  constexpr size_t lds = (S::LFRAGS + 2 * S::STAGE_FRAGS) * 64 * 8 * sizeof(T);  // static LDS of the kernel
+  const int per_cu = lds <= 80 * 1024 ? 2 : 1;
+  const int64_t ngroups = (tokens + S::TPB - 1) / S::TPB;
+  int64_t grid = (int64_t)device_cu_count() * per_cu;
+  if (grid > ngroups) grid = ngroups;
+  hipLaunchKernelGGL((fq_mfma_kernel<DT, MB, NP, PACK>), dim3((unsigned)grid), dim3(S::WAVES * 64), 0, stream,
+                     reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
+                     reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
+  return QO_OK;
+}
+
+template <class DT, bool PACK>
+static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_ld, const void* left,
+                         const void* right, float clip, void* out_codes, float* out_scales,
+                         hipStream_t stream, bool* handled) {
+  *handled = true;
+#define QO_FQ_CASE(MB_, NP_)                                                                      \
+  if (M == 16 * (MB_) && N == 32 * (NP_))                                                         \
+    return launch_mfma<DT, MB_, NP_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, \
+                                           stream);
+  QO_FQ_CASE(4, 2)   // 64 x 64    (hidden 4096)
+  QO_FQ_CASE(7, 4)   // 112 x 128  (hidden 14336)
+  QO_FQ_CASE(2, 2)   // 32 x 64    (hidden 2048)
+  QO_FQ_CASE(4, 4)   // 64 x 128   (hidden 8192)
+  QO_FQ_CASE(8, 4)   // 128 x 128  (hidden 16384)
+  QO_FQ_CASE(2, 1)   // 32 x 32    (hidden 1024)
+  QO_FQ_CASE(3, 2)   // 48 x 64    (hidden 3072)
+  QO_FQ_CASE(5, 2)   // 80 x 64    (hidden 5120)
+  QO_FQ_CASE(6, 4)   // 96 x 128   (hidden 12288)
+#undef QO_FQ_CASE
+  *handled = false;
+  return QO_OK;
+}
+
+template <class DT, bool PACK>
+static int launch_generic(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right,
+                          int M, int N, float clip, void* out_codes, float* out_scales, hipStream_t stream) {
+  using T = typename DT::T;
+  const size_t lds = (size_t)2 * M * N * sizeof(T);
+  auto kern = fq_generic_kernel<DT, PACK>;
+  if (lds > 64 * 1024) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+        hipSuccess) {
+      qo_set_error("qo_flatquant_quantize: M*N=%d needs %zu bytes of LDS", M * N, lds);
+      return QO_ERR_UNSUPPORTED;
+    }
+  }
+  int64_t grid = (int64_t)device_cu_count() * 4;
+  if (grid > tokens) grid = tokens;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), lds, stream, reinterpret_cast<const T*>(x), tokens,
+                     x_ld, reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), M, N, clip,
+                     out_codes, out_scales);
+  return QO_OK;
+}
+
+template <class DT, bool PACK>
+static int run_quantize(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right, int M,
+                        int N, float clip, void* out_codes, float* out_scales, hipStream_t stream,
+                        bool allow_mfma) {
+  if constexpr (DT::code != QO_DTYPE_F32) {
+    const bool aligned = ((uintptr_t)x % 16 == 0) && ((x_ld * (int64_t)sizeof(typename DT::T)) % 16 == 0);
+    if (allow_mfma && aligned) {
+      bool handled = false;
+      int st = dispatch_mfma<DT, PACK>(M, N, x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream,
+                                       &handled);
+      if (handled) return st;
+    }
+  }
+  return launch_generic<DT, PACK>(x, tokens, x_ld, left, right, M, N, clip, out_codes, out_scales, stream);
+}
+
+}  // namespace qo
+
+// Selects the kernel family; QO_FQ_FORCE_GENERIC=1 in the environment routes
+// every shape through the generic kernel (tests use it to cross-check the two).
+static bool fq_allow_mfma() {
+  const char* e = getenv("QO_FQ_FORCE_GENERIC");
+  return !(e && e[0] == '1');
+}
+
+extern "C" int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
+                                     const void* right, int M, int N, float clip_ratio, int pack_int32,
+                                     void* out_codes, float* out_scales, void* stream) {
+  using namespace qo;
+  if (tokens < 0 || M < 1 || N < 1) {
+    qo_set_error("qo_flatquant_quantize: invalid sizes tokens=%lld M=%d N=%d", (long long)tokens, M, N);
+    return QO_ERR_SHAPE;
+  }
+  if (pack_int32 && ((int64_t)M * N) % 8 != 0) {
+    qo_set_error("qo_flatquant_quantize: features (%lld) must be divisible by 8 for int32 packing",
+                 (long long)M * N);
+    return QO_ERR_SHAPE;
+  }
+  if (x_ld < (int64_t)M * N) {
+    qo_set_error("qo_flatquant_quantize: row stride %lld < features %lld", (long long)x_ld, (long long)M * N);
+    return QO_ERR_SHAPE;
+  }
+  if (tokens == 0) return QO_OK;
+  if (!x || !left || !right || !out_codes || !out_scales) {
+    qo_set_error("qo_flatquant_quantize: NULL pointer argument");
+    return QO_ERR_NULL_POINTER;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool mf = fq_allow_mfma();
+  int st;
+  switch (x_dtype) {
+    case QO_DTYPE_F32:
+      st = pack_int32 ? run_quantize<F32T, true>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
+                                                  out_scales, s, mf)
+                      : run_quantize<F32T, false>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
+                                                   out_scales, s, mf);
+      break;
+    case QO_DTYPE_F16:
+      st = pack_int32 ? run_quantize<F16T, true>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
+                                                  out_scales, s, mf)
+                      : run_quantize<F16T, false>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
+                                                   out_scales, s, mf);
+      break;
+    case QO_DTYPE_BF16:
+      st = pack_int32 ? run_quantize<BF16T, true>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
+                                                   out_scales, s, mf)
+                      : run_quantize<BF16T, false>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
+                                                    out_scales, s, mf);
+      break;
+    default:
+      qo_set_error("qo_flatquant_quantize: unsupported input dtype code %d", x_dtype);
+      return QO_ERR_DTYPE;
+  }
+  if (st != QO_OK) return st;
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    qo_set_error("qo_flatquant_quantize: launch failed: %s", hipGetErrorString(e));
+    return QO_ERR_LAUNCH;
+  }
+  return QO_OK;
+}

@@ -1,0 +1,181 @@
+"""Host-side behaviour of the drop-in API and the C ABI (no GPU needed)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+import quant_ops_amd as qo
+from quant_ops_amd import _loader, capi
+from oracle import fq_reference as ofq
+from oracle import int4_reference as oi4
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_public_names_match_reference():
+    # src/quant_ops/__init__.py:39-45
+    assert set(qo.__all__) == {"flatquant_dynamic_quantize", "dequantize_int4", "int4_matmul",
+                               "get_decompose_dim", "CUDA_AVAILABLE"}
+    for name in ("flatquant_cuda", "flatquant_pytorch", "_FlatQuantCUDA", "int4_matmul_cuda",
+                 "int4_matmul_pytorch", "pack_int4_to_int32", "unpack_int32_to_int4", "__version__"):
+        assert hasattr(qo, name), name
+
+
+def test_native_library_loaded_and_schemas_defined():
+    assert _loader.KERNELS_AVAILABLE, _loader.LOAD_ERROR
+    assert qo.CUDA_AVAILABLE
+    ops = torch.ops.quant_ops
+    assert str(ops.flatquant_dynamic_quantize.default._schema) == (
+        "quant_ops::flatquant_dynamic_quantize(Tensor input, Tensor left_trans, Tensor right_trans, "
+        "float clip_ratio=1., bool pack_int32=False) -> (Tensor, Tensor)")
+    assert str(ops.int4_matmul.default._schema) == (
+        "quant_ops::int4_matmul(Tensor a, Tensor b, Tensor scale_a, Tensor scale_b) -> Tensor")
+
+
+def test_c_abi_exports_every_declared_symbol():
+    header = open(os.path.join(ROOT, "include", "quant_ops_hip.h")).read()
+    code = re.sub(r"/\*.*?\*/", "", header, flags=re.S)
+    code = re.sub(r"//[^\n]*", "", code)
+    declared = set(re.findall(r"\b(qo_[a-z0-9_]+)\s*\(", code))
+    assert declared == set(capi.EXPORTED)
+    out = subprocess.run(["nm", "-D", "--defined-only", _loader.HIP_LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert declared <= exported
+    lib = capi.lib()
+    for name in declared:
+        assert getattr(lib, name) is not None
+
+
+def test_c_abi_status_and_errors_without_gpu():
+    lib = capi.lib()
+    assert capi.version() == qo.__version__
+    assert lib.qo_status_string(0) == b"ok"
+    assert lib.qo_status_string(2) == b"invalid shape"
+    # argument checks run before any device work, so they are testable here
+    st = lib.qo_flatquant_quantize(None, 1, 4, 64, None, None, 8, 8, ctypes.c_float(1.0), 1, None, None, None)
+    assert st == 1  # NULL pointer
+    st = lib.qo_flatquant_quantize(None, 1, 4, 12, None, None, 3, 4, ctypes.c_float(1.0), 1, None, None, None)
+    assert st == 2 and b"divisible by 8" in lib.qo_last_error()
+    st = lib.qo_flatquant_quantize(None, 9, 4, 64, None, None, 8, 8, ctypes.c_float(1.0), 0, None, None, None)
+    assert st in (1, 3)
+    st = lib.qo_int4_gemm(None, 1, None, 1, 1, None, 0, None, 0, None, 1, 4, 4, 4, 12, None)
+    assert st == 2 and b"multiple of 8" in lib.qo_last_error()
+    st = lib.qo_int4_gemm(None, 1 << 18, None, 1, 1, None, 0, None, 0, None, 1, 4, 4, 4, 1 << 21, None)
+    assert st == 2
+    st = lib.qo_int4_gemm(None, 1, None, 1, 1, None, 7, None, 0, None, 1, 4, 4, 4, 8, None)
+    assert st == 3
+    st = lib.qo_dequantize_int4(None, 1, None, 0, 4, 12, None, None)
+    assert st == 2
+    # empty problems are valid no-ops
+    assert lib.qo_int4_gemm(None, 1, None, 1, 1, None, 0, None, 0, None, 1, 0, 0, 0, 8, None) == 0
+    assert lib.qo_flatquant_quantize(None, 1, 0, 64, None, None, 8, 8, ctypes.c_float(1.0), 1, None, None,
+                                     None) == 0
+
+
+def _cfg(t=16, m=8, n=8, dtype=torch.float16, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(t, m * n, generator=g) * 2).to(dtype)
+    L = torch.linalg.qr(torch.randn(m, m, generator=g))[0].to(dtype)
+    R = torch.linalg.qr(torch.randn(n, n, generator=g))[0].to(dtype)
+    return x, L, R
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("pack", [False, True])
+def test_cpu_tensors_use_reference_fallback(dtype, pack):
+    x, L, R = _cfg(dtype=dtype)
+    q, s = qo.flatquant_dynamic_quantize(x, L, R, 0.9, pack)
+    q2, s2 = qo.flatquant_dynamic_quantize(x, L, R, 0.9, pack, use_cuda=False)
+    qr, sr = ofq.flatquant_pytorch(x, L, R, 0.9, pack)
+    assert torch.equal(q, qr) and torch.equal(s, sr) and torch.equal(q2, qr) and torch.equal(s2, sr)
+    assert s.dtype == dtype                      # fallback keeps the input dtype (flatquant/ops.py:113)
+    assert q.dtype == (torch.int32 if pack else torch.int8)
+
+
+def test_dequantize_cpu_matches_oracle():
+    x, L, R = _cfg(t=5, m=8, n=16, dtype=torch.bfloat16)
+    for pack in (False, True):
+        q, s = qo.flatquant_dynamic_quantize(x, L, R, 1.0, pack)
+        assert torch.equal(qo.dequantize_int4(q, s, pack), ofq.dequantize_int4(q, s, pack))
+
+
+def test_pack_unpack_match_oracle():
+    g = torch.Generator().manual_seed(3)
+    q = torch.randint(-8, 8, (7, 40), generator=g, dtype=torch.int8)
+    w = qo.pack_int4_to_int32(q)
+    assert np.array_equal(w.numpy(), oi4.pack_int4_to_int32(q.numpy()))
+    assert torch.equal(qo.unpack_int32_to_int4(w), q)
+
+
+def test_int4_matmul_cpu_matches_oracle():
+    g = torch.Generator().manual_seed(4)
+    qa = torch.randint(-8, 8, (9, 64), generator=g, dtype=torch.int8)
+    qb = torch.randint(-8, 8, (64, 11), generator=g, dtype=torch.int8)
+    a = qo.pack_int4_to_int32(qa)
+    b = qo.pack_int4_to_int32(qb.T).T.contiguous()
+    sa = torch.rand(9, generator=g).half()
+    sb = torch.rand(11, generator=g).half()
+    out = qo.int4_matmul(a, b, sa, sb)
+    ref = oi4.int4_matmul_pytorch(a, b, sa, sb)
+    assert out.dtype == torch.float16 and torch.equal(out, ref)
+    assert qo.int4_matmul(a, b, sa, sb, out_dtype=torch.bfloat16).dtype == torch.bfloat16
+
+
+def test_get_decompose_dim():
+    assert qo.get_decompose_dim(4096) == (64, 64)
+    assert qo.get_decompose_dim(2048) == (32, 64)
+    assert qo.get_decompose_dim(14336) == (112, 128)
+    assert qo.get_decompose_dim(0) == (0, 0)
+    with pytest.raises(ValueError):
+        qo.get_decompose_dim(6)
+
+
+def test_gpu_entry_points_refuse_without_kernels(monkeypatch):
+    monkeypatch.setattr(_loader, "KERNELS_AVAILABLE", False)
+    monkeypatch.setattr(_loader, "LOAD_ERROR", "simulated")
+    x, L, R = _cfg()
+    with pytest.raises(RuntimeError, match="not available"):
+        qo.flatquant_cuda(x, L, R)
+    with pytest.raises(RuntimeError, match="not available"):
+        qo.int4_matmul_cuda(torch.zeros(1, 1, dtype=torch.int32), torch.zeros(1, 1, dtype=torch.int32),
+                            torch.ones(1), torch.ones(1))
+    # the CPU path is unaffected
+    qo.flatquant_dynamic_quantize(x, L, R)
+
+
+def test_fake_kernels_give_reference_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        x = torch.empty(6, 64, dtype=torch.float16)
+        L = torch.empty(8, 8, dtype=torch.float16)
+        q, s = torch.ops.quant_ops.flatquant_dynamic_quantize(x, L, L, 0.9, True)
+        assert q.shape == (6, 8) and q.dtype == torch.int32 and s.shape == (6,) and s.dtype == torch.float32
+        q, s = torch.ops.quant_ops.flatquant_dynamic_quantize(x, L, L, 0.9, False)
+        assert q.shape == (6, 64) and q.dtype == torch.int8
+        a = torch.empty(5, 4, dtype=torch.int32)
+        b = torch.empty(4, 7, dtype=torch.int32)
+        o = torch.ops.quant_ops.int4_matmul(a, b, torch.empty(5), torch.empty(7))
+        assert o.shape == (5, 7) and o.dtype == torch.float16
+        o = torch.ops.quant_ops.int4_matmul_ex(a, b, torch.empty(5), torch.empty(7), torch.bfloat16)
+        assert o.dtype == torch.bfloat16
+        d = torch.ops.quant_ops.dequantize_int4(a, torch.empty(5), True)
+        assert d.shape == (5, 32) and d.dtype == torch.float32
+
+
+def test_workload_generators_are_seeded():
+    from quant_ops_amd import workloads as wl
+
+    c1, c2 = wl.quant_cfg2(tokens=8), wl.quant_cfg2(tokens=8)
+    assert torch.equal(c1.x, c2.x) and torch.equal(c1.left, c2.left)
+    assert c1.x.dtype == torch.float16 and c1.pack_int32 and c1.clip_ratio == 0.9
+    full = wl.quant_cfg2()
+    assert full.algorithmic_bytes() == 20_996_096      # X + packed codes + fp32 scales + L, R
+    g = wl.gemm_case(32, 48, 64, b_transposed_view=True)
+    assert g.b.shape == (8, 48) and g.b.stride() == (1, 8)
+    assert wl.gemm_cfg4().ops() == 481_036_337_152

@@ -1,0 +1,317 @@
+"""GPU parity: the HIP kernels (called through the C ABI and through the torch
+operators) against the CPU oracle, on identical seeded inputs.
+
+Bars (north star): packing and int32 GEMM accumulators bit-exact given the same
+codes; codes within 1 of the oracle on at most 0.1 % of elements; scales within
+1e-3 relative; dequantized / GEMM float output within 1e-2 relative. The GEMM
+output is in fact checked bit-exact (same float32 products, one rounding).
+"""
+import pytest
+import torch
+
+import quant_ops_amd as qo
+from quant_ops_amd import capi
+from quant_ops_amd import workloads as wl
+from oracle import fq_reference as ofq
+from oracle import int4_reference as oi4
+
+pytestmark = pytest.mark.gpu
+
+CODE_FLIP_FRAC = 1e-3      # codes may differ by 1 on <= 0.1 % of elements
+SCALE_RTOL = 1e-3
+DEQUANT_RTOL = 1e-2
+
+
+def _say(msg):
+    print(f"[gpu-parity] {msg}", flush=True)
+
+
+def _codes_int8(codes, packed):
+    c = codes.cpu()
+    if packed:
+        return torch.from_numpy(oi4.unpack_int32_to_int4(c.numpy()))
+    return c
+
+
+def check_quant(x, L, R, clip, pack, q_gpu, s_gpu, tag):
+    """Compare kernel output with the oracle; returns (flip fraction, scale bit-equal fraction)."""
+    q_ref, s_ref = ofq.flatquant_pytorch(x, L, R, clip, pack)
+    s_ref32 = s_ref.float()
+    s_g = s_gpu.cpu()
+    assert s_g.dtype == torch.float32 and s_g.shape == s_ref.shape
+    denom = s_ref32.abs().clamp_min(torch.finfo(torch.float32).tiny)
+    srel = ((s_g - s_ref32).abs() / denom)
+    srel = torch.where((s_g == s_ref32), torch.zeros_like(srel), srel)
+    assert float(srel.max()) <= SCALE_RTOL, f"{tag}: scale rel err {float(srel.max())}"
+    qg = _codes_int8(q_gpu, pack).to(torch.int16)
+    qr = _codes_int8(q_ref, pack).to(torch.int16)
+    assert qg.shape == qr.shape
+    d = (qg - qr).abs()
+    assert int(d.max()) <= 1, f"{tag}: code difference {int(d.max())}"
+    flips = float((d != 0).float().mean())
+    assert flips <= CODE_FLIP_FRAC, f"{tag}: {flips:.2e} of codes differ"
+    deq_g = qg.float() * s_g.view(-1, 1)
+    deq_r = qr.float() * s_ref32.view(-1, 1)
+    rel = float((deq_g - deq_r).norm() / deq_r.norm().clamp_min(1e-30))
+    assert rel <= DEQUANT_RTOL, f"{tag}: dequantized rel err {rel}"
+    same = float((s_g == s_ref32).float().mean())
+    _say(f"{tag}: code flips {flips:.2e}, scales bit-equal {same:.4f}, dequant rel {rel:.2e}")
+    return flips, same
+
+
+def run_capi_quant(case, dev, **kw):
+    x = case.x.to(dev)
+    L, R = case.left.to(dev), case.right.to(dev)
+    q, s = capi.flatquant_quantize(x, L, R, case.clip_ratio, case.pack_int32, **kw)
+    torch.cuda.synchronize()
+    return q, s
+
+
+# --------------------------------------------------------------------------- quantize
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
+def test_quantize_baseline_configs(gpu, cfg):
+    case = {"cfg1": wl.quant_cfg1, "cfg2": wl.quant_cfg2, "cfg3": wl.quant_cfg3}[cfg]()
+    _say(f"{case.name}: T={case.tokens} F={case.features} {case.x.dtype} pack={case.pack_int32}")
+    q, s = run_capi_quant(case, gpu)
+    flips, same = check_quant(case.x, case.left, case.right, case.clip_ratio, case.pack_int32, q, s, case.name)
+    # the kernel rounds where the fallback rounds: flips stay far below the bar
+    assert flips <= 2e-4 and same >= 0.99
+
+
+SHAPES = [
+    # (tokens, M, N, dtype, clip, pack)
+    (1, 64, 64, torch.float16, 0.9, True),
+    (3, 64, 64, torch.bfloat16, 1.0, False),
+    (17, 112, 128, torch.bfloat16, 0.9, True),
+    (5, 112, 128, torch.float16, 1.0, False),
+    (33, 32, 64, torch.float16, 0.95, True),
+    (9, 128, 128, torch.bfloat16, 1.0, True),
+    (7, 48, 64, torch.bfloat16, 1.0, True),
+    (6, 96, 128, torch.float16, 0.8, False),
+    (4, 32, 32, torch.float16, 1.0, True),
+    (11, 16, 16, torch.bfloat16, 1.0, True),     # generic kernel (N not a multiple of 32)
+    (2, 8, 8, torch.float16, 0.9, False),        # generic kernel
+    (5, 12, 20, torch.float32, 1.0, False),      # generic kernel, fp32
+    (4, 64, 64, torch.float32, 0.9, True),
+]
+
+
+@pytest.mark.parametrize("t,m,n,dtype,clip,pack", SHAPES)
+def test_quantize_shapes(gpu, t, m, n, dtype, clip, pack):
+    case = wl.quant_case(f"T{t}_{m}x{n}_{str(dtype)[6:]}", t, m, n, dtype, clip, pack, seed=t + m,
+                         outlier_frac=0.01, outlier_scale=20.0)
+    _say(case.name)
+    q, s = run_capi_quant(case, gpu)
+    check_quant(case.x, case.left, case.right, clip, pack, q, s, case.name)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mn", [(64, 64), (112, 128)])
+def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
+    m, n = mn
+    case = wl.quant_case("xcheck", 37, m, n, dtype, 0.9, True, seed=5, outlier_frac=0.005, outlier_scale=30.0)
+    _say(f"mfma vs generic {m}x{n} {dtype}")
+    q1, s1 = run_capi_quant(case, gpu)
+    monkeypatch.setenv("QO_FQ_FORCE_GENERIC", "1")
+    q2, s2 = run_capi_quant(case, gpu)
+    monkeypatch.delenv("QO_FQ_FORCE_GENERIC")
+    d = (_codes_int8(q1, True).int() - _codes_int8(q2, True).int()).abs()
+    assert int(d.max()) <= 1 and float((d != 0).float().mean()) <= CODE_FLIP_FRAC
+    assert float(((s1 - s2).abs() / s2.abs()).max()) <= SCALE_RTOL
+
+
+def test_quantize_zero_and_constant_tokens(gpu):
+    for dtype in (torch.float16, torch.bfloat16):
+        for pack in (False, True):
+            case = wl.quant_case("zeros", 6, 64, 64, dtype, 1.0, pack, seed=1)
+            case.x[0].zero_()
+            case.x[3].zero_()
+            case.x[4].fill_(2.0)
+            _say(f"zero tokens {dtype} pack={pack}")
+            q, s = run_capi_quant(case, gpu)
+            q_ref, s_ref = ofq.flatquant_pytorch(case.x, case.left, case.right, 1.0, pack)
+            # zero rows are exact special cases: fp16 scale 0 with the fallback's
+            # NaN-cast codes, bf16 the 1e-8 floor with code 0
+            for r in (0, 3):
+                assert s.cpu()[r].item() == s_ref[r].float().item()
+                assert torch.equal(q.cpu()[r], q_ref[r]), (dtype, pack, r)
+            check_quant(case.x, case.left, case.right, 1.0, pack, q, s, f"zeros {dtype} {pack}")
+
+
+def test_quantize_strided_rows_and_empty(gpu):
+    case = wl.quant_case("strided", 19, 64, 64, torch.bfloat16, 0.9, True, seed=2)
+    wide = torch.zeros(19, 4096 + 64, dtype=torch.bfloat16)
+    wide[:, :4096] = case.x
+    xs = wide.to(gpu)[:, :4096]
+    assert xs.stride(0) == 4160
+    q, s = capi.flatquant_quantize(xs, case.left.to(gpu), case.right.to(gpu), 0.9, True)
+    torch.cuda.synchronize()
+    check_quant(case.x, case.left, case.right, 0.9, True, q, s, "strided rows")
+    empty = torch.empty(0, 4096, dtype=torch.float16, device=gpu)
+    q, s = capi.flatquant_quantize(empty, case.left.half().to(gpu), case.right.half().to(gpu), 1.0, True)
+    assert q.shape == (0, 512) and s.shape == (0,)
+
+
+def test_quantize_torch_op_matches_capi_and_stream(gpu):
+    case = wl.quant_cfg2(tokens=300, seed=3)
+    x, L, R = case.x.to(gpu), case.left.to(gpu), case.right.to(gpu)
+    q1, s1 = capi.flatquant_quantize(x, L, R, 0.9, True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        q2, s2 = qo.flatquant_dynamic_quantize(x, L, R, 0.9, True)
+        q3, s3 = qo.flatquant_cuda(case.x, case.left, case.right, 0.9, True)   # host inputs moved
+    side.synchronize()
+    torch.cuda.synchronize()
+    assert q2.is_cuda and s2.dtype == torch.float32
+    assert torch.equal(q1, q2) and torch.equal(s1, s2) and torch.equal(q1, q3) and torch.equal(s1, s3)
+    # use_cuda=False keeps the reference fallback semantics (scale in the input dtype)
+    q4, s4 = qo.flatquant_dynamic_quantize(case.x, case.left, case.right, 0.9, True, use_cuda=False)
+    assert s4.dtype == torch.float16
+
+
+def test_quantize_graph_capture_replays(gpu):
+    case = wl.quant_cfg2(tokens=256, seed=4)
+    x, L, R = case.x.to(gpu), case.left.to(gpu), case.right.to(gpu)
+    q_eager, s_eager = qo.flatquant_dynamic_quantize(x, L, R, 0.9, True)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        qo.flatquant_dynamic_quantize(x, L, R, 0.9, True)   # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        q_g, s_g = qo.flatquant_dynamic_quantize(x, L, R, 0.9, True)
+    for i in range(4):
+        q_g.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(q_g, q_eager) and torch.equal(s_g, s_eager), f"replay {i}"
+
+
+# --------------------------------------------------------------------------- dequantize
+
+@pytest.mark.parametrize("pack", [False, True])
+@pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
+def test_dequantize_bit_exact(gpu, pack, sdt):
+    g = torch.Generator().manual_seed(9)
+    q = torch.randint(-8, 8, (37, 4096), generator=g, dtype=torch.int8)
+    s = (torch.rand(37, generator=g) + 0.01).to(sdt)
+    codes = torch.from_numpy(oi4.pack_int4_to_int32(q.numpy())) if pack else q
+    ref = ofq.dequantize_int4(codes, s, pack)
+    out = capi.dequantize_int4(codes.to(gpu), s.to(gpu), pack)
+    out2 = qo.dequantize_int4(codes.to(gpu), s.to(gpu), pack)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), ref) and torch.equal(out2.cpu(), ref)
+
+
+def test_dequantize_odd_features(gpu):
+    q = torch.randint(-8, 8, (5, 13), dtype=torch.int8)
+    s = torch.rand(5) + 0.5
+    out = capi.dequantize_int4(q.to(gpu), s.to(gpu), False)
+    assert torch.equal(out.cpu(), ofq.dequantize_int4(q, s, False))
+
+
+# --------------------------------------------------------------------------- GEMM
+
+def _gemm_ref_acc(a, b):
+    return oi4.int4_matmul_int32(a, b)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 8), (16, 16, 64), (64, 48, 128), (300, 260, 1032), (256, 256, 4096),
+                                   (257, 513, 2056), (33, 7, 72)])
+@pytest.mark.parametrize("bview", [False, True])
+def test_gemm_small_bit_exact(gpu, m, n, k, bview):
+    case = wl.gemm_case(m, n, k, seed=m + n + k, b_transposed_view=bview)
+    _say(f"gemm {m}x{n}x{k} bview={bview}")
+    ref = oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b)
+    a, b = case.a.to(gpu), case.b.to(gpu)
+    if bview:
+        assert b.stride(0) == 1
+    out = capi.int4_gemm(a, b, case.scale_a.to(gpu), case.scale_b.to(gpu))
+    # integer accumulators through a float32 output with unit scales
+    one_a = torch.ones(m, device=gpu)
+    one_b = torch.ones(n, device=gpu)
+    acc = capi.int4_gemm(a, b, one_a, one_b, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(acc.cpu().to(torch.int64), _gemm_ref_acc(case.a, case.b).to(torch.int64))
+    assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
+def test_gemm_scale_and_out_dtypes(gpu, sdt, odt):
+    case = wl.gemm_case(96, 160, 512, seed=11)
+    sa, sb = case.scale_a.to(sdt), case.scale_b.to(sdt)
+    ref = oi4.int4_matmul_pytorch(case.a, case.b, sa, sb, out_dtype=odt)
+    out = qo.int4_matmul(case.a.to(gpu), case.b.to(gpu), sa.to(gpu), sb.to(gpu), out_dtype=odt)
+    torch.cuda.synchronize()
+    assert out.dtype == odt and torch.equal(out.cpu(), ref)
+
+
+def test_gemm_fast_matches_generic(gpu, monkeypatch):
+    case = wl.gemm_case(512, 384, 2048, seed=12, b_transposed_view=True)
+    args = (case.a.to(gpu), case.b.to(gpu), case.scale_a.to(gpu), case.scale_b.to(gpu))
+    o1 = capi.int4_gemm(*args)
+    monkeypatch.setenv("QO_GEMM_FORCE_GENERIC", "1")
+    o2 = capi.int4_gemm(*args)
+    monkeypatch.delenv("QO_GEMM_FORCE_GENERIC")
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+
+def test_gemm_cfg4_full_size(gpu):
+    case = wl.gemm_cfg4()
+    _say(case.name)
+    a, b = case.a.to(gpu), case.b.to(gpu)
+    out = capi.int4_gemm(a, b, case.scale_a.to(gpu), case.scale_b.to(gpu))
+    torch.ops.quant_ops.int4_matmul(a, b, case.scale_a.to(gpu), case.scale_b.to(gpu))
+    torch.cuda.synchronize()
+    rows = torch.arange(0, 4096, 17)                      # spread over every tile row position
+    ref = oi4.int4_matmul_pytorch(case.a[rows], case.b, case.scale_a[rows], case.scale_b)
+    assert torch.equal(out.cpu()[rows], ref)
+    # every accumulator, through exact row and column checksums:
+    # sum_m acc[m, n] = (sum_m qa[m, :]) . qb[:, n] and sum_n acc[m, n] = qa[m, :] . (sum_n qb[:, n])
+    acc = capi.int4_gemm(a, b, torch.ones(4096, device=gpu), torch.ones(14336, device=gpu),
+                         out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    acc64 = acc.to(torch.float64)
+    qa = torch.from_numpy(oi4.unpack_int32_to_int4(case.a.numpy())).to(torch.float64)
+    qb = torch.from_numpy(oi4.unpack_int32_to_int4(case.b.T.contiguous().numpy())).T.to(torch.float64)
+    col = acc64.sum(0).cpu()
+    row = acc64.sum(1).cpu()
+    assert torch.equal(col, qa.sum(0) @ qb)
+    assert torch.equal(row, qa @ qb.sum(1))
+
+
+def test_gemm_rejects_bad_shapes(gpu):
+    a = torch.zeros(4, 2, dtype=torch.int32, device=gpu)
+    b = torch.zeros(3, 5, dtype=torch.int32, device=gpu)
+    with pytest.raises(RuntimeError, match="mismatch"):
+        qo.int4_matmul(a, b, torch.ones(4, device=gpu), torch.ones(5, device=gpu))
+    with pytest.raises(RuntimeError):
+        qo.int4_matmul(a.float(), b, torch.ones(4, device=gpu), torch.ones(5, device=gpu))
+
+
+# --------------------------------------------------------------------------- end to end (config 5)
+
+@pytest.mark.parametrize("tokens", [16, 4096])
+def test_w4a4_linear_down_proj(gpu, tokens):
+    x = wl.activations(tokens, 14336, torch.bfloat16, seed=21, outlier_frac=0.005, outlier_scale=30.0)
+    L, R = wl.orthogonal(112, 22, torch.bfloat16), wl.orthogonal(128, 23, torch.bfloat16)
+    w = wl.random_packed(4096, 1792, 24)          # [out, in/8]
+    sw = wl.uniform(4096, 0.001, 0.01, 25)
+    _say(f"w4a4 linear T={tokens}")
+    q, s = qo.flatquant_dynamic_quantize(x.to(gpu), L.to(gpu), R.to(gpu), 0.9, True)
+    out = qo.int4_matmul(q, w.to(gpu).t(), s, sw.to(gpu), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    check_quant(x, L, R, 0.9, True, q, s, f"linear T={tokens} quantize")
+    # GEMM stage bit-exact given the kernel's own codes and scales (sampled rows
+    # at the prefill size to bound the CPU time)
+    rows = torch.arange(0, tokens, 1 if tokens <= 64 else 13)
+    ref = oi4.int4_matmul_pytorch(q.cpu()[rows], w.t(), s.cpu()[rows], sw, out_dtype=torch.bfloat16)
+    assert out.shape == (tokens, 4096) and out.dtype == torch.bfloat16
+    assert torch.equal(out.cpu()[rows], ref)
