@@ -41,7 +41,7 @@ def flatquant_pytorch(x, left, right, clip_ratio=1.0, pack_int32=False):
     if not pack_int32:
         return codes.to(torch.int8), scale
     offs = (codes + 8).to(torch.uint8).view(tokens, feats // 8, 8)
-    word = torch.zeros(tokens, feats // 8, dtype=torch.int32)
+    word = torch.zeros(tokens, feats // 8, dtype=torch.int32, device=x.device)
     for i in range(8):
         word += offs[:, :, i].to(torch.int32) << (4 * i)
     return word, scale
@@ -57,6 +57,40 @@ def dequantize_int4(quantized, scales, packed_int32=False):
     if packed_int32:
         q = torch.from_numpy(unpack_int32_to_int4(quantized.cpu().numpy()))
     return q.float() * scales.view(-1, 1).expand_as(q)
+
+
+def flatquant_sequential(x, left, right, clip_ratio=1.0, pack_int32=False):
+    """The fallback with its two GEMMs pinned to sequential float32 accumulation.
+
+    ``flatquant_pytorch`` inherits the host BLAS's summation order: torch's CPU
+    half/bfloat16 GEMM accumulates k = 0, 1, 2, ... in float32 on the Intel
+    AVX-512 host this suite is developed on (bit-identical to this function),
+    while on an AMD EPYC host the first product uses four interleaved float32
+    accumulators (k mod 4). This variant fixes the order (products of D values
+    are exact in float32, so each step is one float32 rounding) and then applies
+    the fallback's scale/quantize steps unchanged, giving a host-independent
+    reference for the kernels' rounding points.
+    """
+    tokens, feats = x.shape
+    m, n = left.shape[0], right.shape[0]
+    dt = x.dtype
+    xb = x.reshape(-1, m, n).float()
+    rf, lf = right.float(), left.float()
+    acc = torch.zeros(xb.shape[0], m, n, dtype=torch.float32)
+    for k in range(n):
+        acc = acc + xb[:, :, k:k + 1] * rf[k:k + 1, :]
+    z = acc.to(dt).float()
+    acc = torch.zeros_like(acc)
+    for k in range(m):
+        acc = acc + lf[k].view(1, m, 1) * z[:, k:k + 1, :]
+    y = acc.to(dt).reshape(tokens, feats)
+    hi = y.amax(dim=1, keepdim=True)
+    lo = y.amin(dim=1, keepdim=True)
+    scale = (torch.maximum((lo * clip_ratio).abs(), hi * clip_ratio) / 7.0).clamp(min=1e-8).squeeze(1)
+    codes = torch.round(y / scale.view(-1, 1).expand_as(y)).clamp(-8, 7)
+    if not pack_int32:
+        return codes.to(torch.int8), scale
+    return torch.from_numpy(pack_int4_to_int32(codes.to(torch.int8).numpy())), scale
 
 
 # ---------------------------------------------------------------------------

@@ -33,6 +33,9 @@ HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    # no implicit contraction: the reference rounds every float32 product before
+    # rounding to half, and a fused mul-convert (v_fma_mixlo_f16) rounds once
+    "-ffp-contract=off",
     # packed fp32 VALU forms are kept out of every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",

@@ -79,8 +79,15 @@ def version() -> str:
 
 def flatquant_quantize(x, left, right, clip_ratio=1.0, pack_int32=False, out_codes=None, out_scales=None,
                        stream=None):
-    """Call ``qo_flatquant_quantize`` on device tensors; allocates outputs if not given."""
+    """Call ``qo_flatquant_quantize`` on device tensors; allocates outputs if not given.
+
+    The C ABI reads L and R as row-major [M, M] / [N, N]; other layouts (e.g. the
+    column-major Q that torch.linalg.qr returns) are made contiguous here.
+    """
     t, f = x.shape
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    left, right = left.contiguous(), right.contiguous()
     m, n = left.shape[0], right.shape[0]
     if out_codes is None:
         out_codes = torch.empty((t, f // 8) if pack_int32 else (t, f),
@@ -98,6 +105,11 @@ def flatquant_quantize(x, left, right, clip_ratio=1.0, pack_int32=False, out_cod
 def int4_gemm(a, b, scale_a, scale_b, out_dtype=torch.float16, out=None, stream=None):
     """Call ``qo_int4_gemm``; ``b`` may be row-major [K/8, N] or the ``W.t()`` view."""
     m, kp = a.shape
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    if b.stride(0) != 1 and b.stride(1) != 1:
+        b = b.contiguous()
+    scale_a, scale_b = scale_a.contiguous(), scale_b.contiguous()
     n = b.shape[1]
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=a.device)
@@ -113,6 +125,7 @@ def int4_gemm(a, b, scale_a, scale_b, out_dtype=torch.float16, out=None, stream=
 
 def dequantize_int4(codes, scales, packed_int32=False, out=None, stream=None):
     """Call ``qo_dequantize_int4``; returns float32 [T, F]."""
+    codes, scales = codes.contiguous(), scales.contiguous()
     t = codes.shape[0]
     f = codes.shape[1] * (8 if packed_int32 else 1)
     if out is None:

@@ -15,6 +15,16 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
+// Hides a value's provenance from the optimizer. The reference rounds every
+// float32 result to the input dtype as a separate step; without this barrier
+// the backend folds (half)(a * b) and (half)fma(a, b, c) into v_fma_mix*_f16
+// (one rounding of the exact result) and narrows (half)(a / b) of widened
+// halves into a half-precision divide, both of which can round differently.
+__device__ inline float opaque(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Element traits: storage type, conversion to float and round-to-nearest-even
 // from float. `round` returns the D-rounded value as a float, which is what
 // the reference fallback holds after every torch op on a D tensor.
@@ -30,16 +40,16 @@ struct F16T {
   using T = _Float16;
   static constexpr int code = QO_DTYPE_F16;
   __device__ static inline float to_f(T v) { return (float)v; }
-  __device__ static inline T from_f(float v) { return (T)v; }
-  __device__ static inline float round(float v) { return (float)(_Float16)v; }
+  __device__ static inline T from_f(float v) { return (T)opaque(v); }
+  __device__ static inline float round(float v) { return (float)(_Float16)opaque(v); }
 };
 
 struct BF16T {
   using T = __bf16;
   static constexpr int code = QO_DTYPE_BF16;
   __device__ static inline float to_f(T v) { return (float)v; }
-  __device__ static inline T from_f(float v) { return (T)v; }
-  __device__ static inline float round(float v) { return (float)(__bf16)v; }
+  __device__ static inline T from_f(float v) { return (T)opaque(v); }
+  __device__ static inline float round(float v) { return (float)(__bf16)opaque(v); }
 };
 
 // Load a scalar of a runtime dtype code (F32/F16/BF16) as float.

@@ -36,7 +36,7 @@ __device__ inline float fq_scale(float ymax_raw, float ymin_raw, float clip) {
   const float t_lo = DT::round(lo * clip);
   const float t_hi = DT::round(hi * clip);
   const float bound = fmaxf(fabsf(t_lo), t_hi);
-  const float s = DT::round(bound / 7.0f);
+  const float s = DT::round(opaque(bound) / 7.0f);
   return fmaxf(s, DT::round(1e-8f));
 }
 
@@ -112,7 +112,7 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
         uint32_t word = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float q = DT::round(DT::to_f(xs[8 * p + i]) / s);
+          const float q = DT::round(opaque(DT::to_f(xs[8 * p + i])) / s);
           word |= (uint32_t)(fq_code_from_quot<true>(q) + 8) << (4 * i);
         }
         o[p] = (int32_t)word;
@@ -120,7 +120,7 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
     } else {
       int8_t* o = reinterpret_cast<int8_t*>(out_codes) + t * F;
       for (int f = tid; f < F; f += 256) {
-        const float q = DT::round(DT::to_f(xs[f]) / s);
+        const float q = DT::round(opaque(DT::to_f(xs[f])) / s);
         o[f] = (int8_t)fq_code_from_quot<false>(q);
       }
     }
@@ -290,7 +290,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) code[j] = fq_code_from_quot<PACK>(DT::round(yv[mb][j] / s));
+      for (int j = 0; j < 8; ++j) code[j] = fq_code_from_quot<PACK>(DT::round(opaque(yv[mb][j]) / s));
     }
     if (PACK) {
       uint32_t word = 0;

@@ -26,13 +26,14 @@
 
 namespace qo {
 
+// Conversions start from a materialised float32 (see opaque()).
 struct OutF16 {
   using T = _Float16;
-  __device__ static inline T cvt(float v) { return (T)v; }
+  __device__ static inline T cvt(float v) { return (T)opaque(v); }
 };
 struct OutBF16 {
   using T = __bf16;
-  __device__ static inline T cvt(float v) { return (T)v; }
+  __device__ static inline T cvt(float v) { return (T)opaque(v); }
 };
 struct OutF32 {
   using T = float;

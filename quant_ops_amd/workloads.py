@@ -23,7 +23,7 @@ def orthogonal(n: int, seed: int, dtype=torch.float32) -> torch.Tensor:
     """Q of the QR factorisation of a seeded N(0, 1) n x n matrix, cast to ``dtype``."""
     g = torch.Generator().manual_seed(seed)
     q, _ = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float32))
-    return q.to(dtype)
+    return q.to(dtype).contiguous()      # QR returns Q column-major
 
 
 def activations(tokens: int, features: int, dtype, seed: int, outlier_frac: float = 0.0,

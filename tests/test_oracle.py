@@ -214,3 +214,33 @@ def test_dequantize_closed_form():
     assert out.tolist() == [[-2.0, 1.75, 0.0, 0.25, -0.25, 0.75, -0.75, 1.25]]
     packed = torch.from_numpy(oi4.pack_int4_to_int32(q.numpy()))
     assert torch.equal(ofq.dequantize_int4(packed, s, True), out)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_sequential_variant_matches_closed_form(dtype):
+    # sequential float32 accumulation written out element by element on a tiny case
+    x, L, R = _case(3, 4, 8, dtype, seed=13, outliers=True)
+    q, s = ofq.flatquant_sequential(x, L, R, 0.9, True)
+    xd = x.reshape(3, 4, 8).double().numpy()
+    Ld, Rd = L.double().numpy(), R.double().numpy()
+    z = np.zeros((3, 4, 8))
+    for t in range(3):
+        for i in range(4):
+            for j in range(8):
+                acc = np.float32(0)
+                for k in range(8):
+                    acc = np.float32(acc + np.float32(xd[t, i, k] * Rd[k, j]))
+                z[t, i, j] = acc
+    zd = torch.from_numpy(z).float().to(dtype).double().numpy()
+    y = np.zeros((3, 4, 8))
+    for t in range(3):
+        for i in range(4):
+            for j in range(8):
+                acc = np.float32(0)
+                for k in range(4):
+                    acc = np.float32(acc + np.float32(Ld[k, i] * zd[t, k, j]))
+                y[t, i, j] = acc
+    yd = torch.from_numpy(y.reshape(3, 32)).float().to(dtype).double().numpy()
+    s_cf, q_cf = ofq.quantize_rows_closed_form(yd, dtype, 0.9)
+    np.testing.assert_array_equal(s.double().numpy(), s_cf)
+    np.testing.assert_array_equal(oi4.unpack_int32_to_int4(q.numpy()), q_cf.astype(np.int8))
