@@ -167,6 +167,68 @@ struct MfmaOps<BF16T> {
   }
 };
 
+// Epilogue on packed pairs. A lane's Y values come in pairs (MFMA block h = 0
+// and 1 at the same accumulator row r) that belong in nibbles r and r + 4 of
+// one output word, so each pair is kept as two 16-bit D values in one VGPR
+// (rounding point 2 for both with one v_cvt_pk). Quantizing a pair:
+//   a = clamp(y * rcp, -8, 7) in float32   (clamp commutes with the roundings
+//                                           below because -8 and 7 are D values)
+//   t = rnd_D(a)                           (one v_cvt_pk for the pair)
+//   t + magic                              (round half to even to an integer)
+// The magic constant leaves q + 8 in the low bits of each result; shifting the
+// pair's bits by 4r and adding puts both codes in place, and the constant bits
+// the magic leaves above the codes add up to kJunk, removed once per word.
+// y * rcp stands in for the fallback's y / s (IEEE): the two differ only when
+// the quotient lies within a few float32 ulps of a rounding boundary of D.
+template <class DT>
+struct FqEpi;
+
+template <>
+struct FqEpi<F16T> {
+  __device__ static inline uint32_t pack(float a, float b) {
+    const v2h h = {(_Float16)opaque(a), (_Float16)opaque(b)};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  __device__ static inline float lo(uint32_t p) { return (float)__builtin_bit_cast(v2h, p)[0]; }
+  __device__ static inline float hi(uint32_t p) { return (float)__builtin_bit_cast(v2h, p)[1]; }
+  // fp16: 1544 = 1536 + 8 has a unit ulp, so t + 1544 is the integer 1536 + q + 8,
+  // bits 0x6600 + (q + 8); both halves are handled by one v_pk_add_f16.
+  __device__ static inline void accumulate(uint32_t& word, uint32_t p, float rcp, int r) {
+    const float a0 = __builtin_amdgcn_fmed3f(lo(p) * rcp, -8.0f, 7.0f);
+    const float a1 = __builtin_amdgcn_fmed3f(hi(p) * rcp, -8.0f, 7.0f);
+    v2h t = __builtin_bit_cast(v2h, pack(a0, a1));
+    const v2h magic = {(_Float16)1544.0f, (_Float16)1544.0f};
+    t = t + magic;
+    word += __builtin_bit_cast(uint32_t, t) << (4 * r);
+  }
+  static constexpr uint32_t kJunk =
+      0x66006600u + (0x66006600u << 4) + (0x66006600u << 8) + (0x66006600u << 12);
+};
+
+template <>
+struct FqEpi<BF16T> {
+  __device__ static inline uint32_t pack(float a, float b) {
+    const v2bf h = {(__bf16)opaque(a), (__bf16)opaque(b)};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  __device__ static inline float lo(uint32_t p) { return __builtin_bit_cast(float, p << 16); }
+  __device__ static inline float hi(uint32_t p) { return __builtin_bit_cast(float, p & 0xFFFF0000u); }
+  // bf16: rounded pair back to float32, then + 12582920 = 1.5 * 2^23 + 8 leaves
+  // bits 0x4B400000 + (q + 8). The high element is shifted by 16 + 4r, which
+  // drops all of 0x4B400000; the low element's constant part sums to kJunk.
+  __device__ static inline void accumulate(uint32_t& word, uint32_t p, float rcp, int r) {
+    const float a0 = __builtin_amdgcn_fmed3f(lo(p) * rcp, -8.0f, 7.0f);
+    const float a1 = __builtin_amdgcn_fmed3f(hi(p) * rcp, -8.0f, 7.0f);
+    const uint32_t t = pack(a0, a1);
+    const float f0 = lo(t) + 12582920.0f;
+    const float f1 = hi(t) + 12582920.0f;
+    word += __builtin_bit_cast(uint32_t, f0) << (4 * r);
+    word += __builtin_bit_cast(uint32_t, f1) << (16 + 4 * r);
+  }
+  static constexpr uint32_t kJunk =
+      0x4B400000u + (0x4B400000u << 4) + (0x4B400000u << 8) + (0x4B400000u << 12);
+};
+
 template <int MB, int NP>
 struct FqShape {
   static constexpr int M = 16 * MB;
@@ -242,7 +304,8 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
   }
 
   // Second product, transposed: Y^T[n][m] = sum_m' Z[m'][n] L[m'][m].
-  float yv[MB][8];
+  using Epi = FqEpi<DT>;
+  uint32_t yp[MB][4];
   float hi = -INFINITY, lo = INFINITY;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -255,10 +318,11 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      // extremes of the raw accumulators: rounding is monotonic, so the D
+      // rounding of these equals amax/amin of the rounded Y
       hi = fmaxf(hi, fmaxf(acc0[r], acc1[r]));
       lo = fminf(lo, fminf(acc0[r], acc1[r]));
-      yv[mb][r] = DT::round(acc0[r]);  // rounding point 2
-      yv[mb][4 + r] = DT::round(acc1[r]);
+      yp[mb][r] = Epi::pack(acc0[r], acc1[r]);  // rounding point 2
     }
   }
 
@@ -277,20 +341,34 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
   const float s = fq_scale<DT>(hi, lo, clip);
   if (t >= tokens) return;
   if (q == 0 && lane == 0) out_scales[t] = s;
+  if (PACK && s > 0.f) {
+    const float rcp = 1.0f / s;
+    int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + 4 * q + lg;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      uint32_t word = 0u - Epi::kJunk;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Epi::accumulate(word, yp[mb][r], rcp, r);
+      orow[(16 * mb + li) * (N / 8)] = (int32_t)word;
+    }
+    return;
+  }
+  // int8 codes, and tokens whose scale rounded to 0 (the fallback's 0/0 codes)
   const float rcp = 1.0f / s;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = 16 * mb + li;
     int code[8];
-    if (s > 0.f) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float tq = DT::round(yv[mb][j] * rcp);
-        code[j] = (int)__builtin_rintf(fminf(fmaxf(tq, -8.0f), 7.0f));
+    for (int r = 0; r < 4; ++r) {
+      const float y0 = Epi::lo(yp[mb][r]), y1 = Epi::hi(yp[mb][r]);
+      if (s > 0.f) {
+        code[r] = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y0 * rcp, -8.0f, 7.0f)));
+        code[4 + r] = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y1 * rcp, -8.0f, 7.0f)));
+      } else {
+        code[r] = fq_code_from_quot<PACK>(DT::round(opaque(y0) / s));
+        code[4 + r] = fq_code_from_quot<PACK>(DT::round(opaque(y1) / s));
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) code[j] = fq_code_from_quot<PACK>(DT::round(opaque(yv[mb][j]) / s));
     }
     if (PACK) {
       uint32_t word = 0;
@@ -335,29 +413,6 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   const int li = lane & 15;    // lane row / column inside a 16x16 block
   const int lg = lane >> 4;    // lane group: k values 8*lg .. 8*lg+7
 
-  // L as B-operand fragments of the second product: fragment (mb, s), lane l,
-  // element j holds L[m'][m], m = 16mb + l%16, m' = 32s + 16(j/4) + 4(l/16) + j%4
-  // (zero for m' >= M). This m' order is the row order of Z's accumulator pairs.
-  for (int e = tid; e < S::LFRAGS * 64 * 8; e += S::WAVES * 64) {
-    const int j = e & 7, l = (e >> 3) & 63, fr = e >> 9;
-    const int mb = fr / KS2, s = fr % KS2;
-    const int m = 16 * mb + (l & 15);
-    const int mp = 32 * s + 16 * (j >> 2) + 4 * (l >> 4) + (j & 3);
-    lfrag[e] = (mp < M) ? left[mp * M + m] : DT::from_f(0.f);
-  }
-
-  // R as B-operand fragments of the first product for this wave's pair:
-  // rf[h][ks][j] = R[32ks + 8lg + j][n], n = 32q + 8(li/4) + 4h + li%4.
-  V rf[2][KS1];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int n = 32 * q + 8 * (li >> 2) + 4 * h + (li & 3);
-#pragma unroll
-    for (int ks = 0; ks < KS1; ++ks)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) rf[h][ks][j] = right[(32 * ks + 8 * lg + j) * N + n];
-  }
-
   // LDS-DMA of one token group into a stage. Fragment c of the stage is token
   // slot c / XFRAGS, block (rb, ks); lane l fetches X[16rb + l%16][32ks + 8(l/16) .. +7]
   // (16 bytes), which the hardware writes to fragment base + 16*l.
@@ -387,7 +442,43 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   };
 
   int64_t g = blockIdx.x;
-  if (g < ngroups) issue(g, xbuf0);
+  if (g < ngroups) issue(g, xbuf0);   // first X group in flight while L and R are fetched
+
+  // L as B-operand fragments of the second product: fragment (mb, s), lane l,
+  // element j holds L[m'][m], m = 16mb + l%16, m' = 32s + 16(j/4) + 4(l/16) + j%4
+  // (zero for m' >= M). This m' order is the row order of Z's accumulator pairs.
+  // All gathers are issued before any LDS store so their latencies overlap.
+  constexpr int LITERS = (S::LFRAGS * 512 + S::WAVES * 64 - 1) / (S::WAVES * 64);
+  T lval[LITERS];
+#pragma unroll
+  for (int i = 0; i < LITERS; ++i) {
+    const int e = tid + i * S::WAVES * 64;
+    const int j = e & 7, l = (e >> 3) & 63, fr = e >> 9;
+    const int mb = fr / KS2, s = fr % KS2;
+    const int m = 16 * mb + (l & 15);
+    const int mp = 32 * s + 16 * (j >> 2) + 4 * (l >> 4) + (j & 3);
+    const bool inside = e < S::LFRAGS * 512 && mp < M;
+    const T v = left[inside ? mp * M + m : 0];   // unconditional load: no branch, no serialising wait
+    lval[i] = inside ? v : DT::from_f(0.f);
+  }
+#pragma unroll
+  for (int i = 0; i < LITERS; ++i) {
+    const int e = tid + i * S::WAVES * 64;
+    if (e < S::LFRAGS * 512) lfrag[e] = lval[i];
+  }
+
+  // R as B-operand fragments of the first product for this wave's pair:
+  // rf[h][ks][j] = R[32ks + 8lg + j][n], n = 32q + 8(li/4) + 4h + li%4.
+  V rf[2][KS1];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int n = 32 * q + 8 * (li >> 2) + 4 * h + (li & 3);
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rf[h][ks][j] = right[(32 * ks + 8 * lg + j) * N + n];
+  }
+
   lds_barrier();  // lfrag visible
 
   while (g < ngroups) {
