@@ -17,6 +17,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace qo {
@@ -151,19 +153,32 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
 template <class DT>
 struct MfmaOps;
 
+// V: 8-element operands of the 16x16x32 MFMA; V4: 4-element operands of the
+// 16x16x16 MFMA, used for an odd trailing 16-deep slab of the second product
+// (lane group g then holds k = 4g .. 4g+3, the same rows as Z's accumulator).
 template <>
 struct MfmaOps<F16T> {
   using V = v8h;
+  using V4 = v4h;
   __device__ static inline v4f mfma(V a, V b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline v4f mfma16(V4 a, V4 b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
   }
 };
 
 template <>
 struct MfmaOps<BF16T> {
   using V = v8bf;
+  using V4 = v4bf;
   __device__ static inline v4f mfma(V a, V b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline v4f mfma16(V4 a, V4 b, v4f c) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, a), __builtin_bit_cast(v4s, b), c, 0,
+                                                     0, 0);
   }
 };
 
@@ -235,16 +250,20 @@ struct FqShape {
   static constexpr int N = 32 * NP;
   static constexpr int F = M * N;
   static constexpr int KS1 = NP;             // 32-deep slabs of the first product (k = n')
-  static constexpr int KS2 = (MB + 1) / 2;   // 32-deep slabs of the second product (k = m')
+  static constexpr int KS2 = MB / 2;         // full 32-deep slabs of the second product (k = m')
+  static constexpr bool TAIL = (MB & 1) != 0; // plus one 16-deep slab when M is an odd multiple of 16
   static constexpr int XFRAGS = MB * KS1;    // 1 KiB A fragments per token
-  // 8 waves unless the X double buffer + L would not fit in 160 KiB of LDS.
-  static constexpr int WAVES = (16 * MB + MB * KS2 <= 150) ? 8 : 4;
-  static constexpr int TPB = WAVES / NP;     // tokens per block iteration
+  // Four waves per workgroup: one token per group at N = 128, two at N = 64,
+  // four at N = 32. Small workgroups (X double buffer only, L in VGPRs) let
+  // several run per CU, so one group's MFMA phase overlaps another's epilogue.
+  static constexpr int TPB = NP >= 4 ? 1 : 4 / NP;   // tokens per group
+  static constexpr int WAVES = NP * TPB;
   static constexpr int STAGE_FRAGS = TPB * XFRAGS;
-  static constexpr int DMA_PER_WAVE = STAGE_FRAGS / WAVES;
-  static constexpr int LFRAGS = MB * KS2;
-  static_assert(WAVES % NP == 0, "waves per block must be a multiple of pairs per token");
+  static constexpr int DMA_PER_WAVE = STAGE_FRAGS / WAVES;   // == MB
+  static constexpr int STAGE_ELEMS = STAGE_FRAGS * 512;
   static_assert(STAGE_FRAGS % WAVES == 0, "X fragments must split evenly over waves");
+  static_assert(M * M <= STAGE_ELEMS, "L must fit in one X stage while it is staged");
+  static_assert(DMA_PER_WAVE < 64, "vmcnt range");
 };
 
 // Wait until at most N vector-memory operations of this wave are outstanding.
@@ -266,7 +285,8 @@ __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 // both products, the per-token scale and the codes.
 template <class DT, int MB, int NP, bool PACK>
 __device__ __attribute__((always_inline)) inline void fq_mfma_group(
-    const typename DT::T* __restrict__ xs, const typename DT::T* __restrict__ lfrag,
+    const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FqShape<MB, NP>::KS2 + 1],
+    const typename MfmaOps<DT>::V4 (&lt)[MB],
     const typename MfmaOps<DT>::V (&rf)[2][FqShape<MB, NP>::KS1], float (*red)[NP][2], int64_t t,
     int64_t tokens, float clip, void* __restrict__ out_codes, float* __restrict__ out_scales, int lane,
     int tau, int q) {
@@ -278,7 +298,9 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
   const int li = lane & 15, lg = lane >> 4;
 
   // First product, one 16-row block of Z at a time: Z[rb] = X[rb] R[:, pair].
-  V zp[2][KS2];
+  using V4 = typename Ops::V4;
+  V zp[2][KS2 + 1];   // full 32-deep slabs of Z^T (one spare entry keeps the array non-empty)
+  V4 zt[2];           // odd trailing 16-row block of Z, when M / 16 is odd
 #pragma unroll
   for (int rb = 0; rb < MB; ++rb) {
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
@@ -291,16 +313,17 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     // Rounding point 1, and the accumulator -> A-operand hand-off.
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      zp[0][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc0[r]);
-      zp[1][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc1[r]);
+      if (S::TAIL && rb == MB - 1) {
+        zt[0][r] = DT::from_f(acc0[r]);
+        zt[1][r] = DT::from_f(acc1[r]);
+      } else {
+        zp[0][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc0[r]);
+        zp[1][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc1[r]);
+      }
     }
-  }
-  if (MB & 1) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      zp[0][KS2 - 1][4 + r] = DT::from_f(0.f);
-      zp[1][KS2 - 1][4 + r] = DT::from_f(0.f);
-    }
+    // keep the scheduler from hoisting every row block's fragment loads at once
+    // (their VGPRs would not fit next to L's and R's fragments)
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // Second product, transposed: Y^T[n][m] = sum_m' Z[m'][n] L[m'][m].
@@ -312,9 +335,12 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS2; ++s) {
-      const V b = *reinterpret_cast<const V*>(lfrag + ((mb * KS2 + s) * 64 + lane) * 8);
-      acc0 = Ops::mfma(zp[0][s], b, acc0);
-      acc1 = Ops::mfma(zp[1][s], b, acc1);
+      acc0 = Ops::mfma(zp[0][s], lf[mb][s], acc0);
+      acc1 = Ops::mfma(zp[1][s], lf[mb][s], acc1);
+    }
+    if (S::TAIL) {
+      acc0 = Ops::mfma16(zt[0], lt[mb], acc0);
+      acc1 = Ops::mfma16(zt[1], lt[mb], acc1);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -389,7 +415,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
 }
 
 template <class DT, int MB, int NP, bool PACK>
-__global__ void __launch_bounds__((FqShape<MB, NP>::WAVES * 64))
+__global__ void __launch_bounds__((FqShape<MB, NP>::WAVES * 64)) __attribute__((amdgpu_waves_per_eu(2)))
 fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
                const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right,
                float clip, void* __restrict__ out_codes, float* __restrict__ out_scales) {
@@ -397,12 +423,12 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   using T = typename DT::T;
   using V = typename MfmaOps<DT>::V;
   constexpr int M = S::M, N = S::N, KS1 = S::KS1, KS2 = S::KS2;
+  constexpr int NT = S::WAVES * 64;
 
   // Two X stages as distinct objects: the compiler then knows that reading one
   // stage does not depend on the LDS-DMA still writing the other.
-  __shared__ __align__(16) T lfrag[S::LFRAGS * 64 * 8];
-  __shared__ __align__(16) T xbuf0[S::STAGE_FRAGS * 64 * 8];
-  __shared__ __align__(16) T xbuf1[S::STAGE_FRAGS * 64 * 8];
+  __shared__ __align__(16) T xbuf0[S::STAGE_ELEMS];
+  __shared__ __align__(16) T xbuf1[S::STAGE_ELEMS];
   __shared__ float red[S::TPB][NP][2];
 
   const int tid = threadIdx.x;
@@ -442,33 +468,11 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   };
 
   int64_t g = blockIdx.x;
-  if (g < ngroups) issue(g, xbuf0);   // first X group in flight while L and R are fetched
-
-  // L as B-operand fragments of the second product: fragment (mb, s), lane l,
-  // element j holds L[m'][m], m = 16mb + l%16, m' = 32s + 16(j/4) + 4(l/16) + j%4
-  // (zero for m' >= M). This m' order is the row order of Z's accumulator pairs.
-  // All gathers are issued before any LDS store so their latencies overlap.
-  constexpr int LITERS = (S::LFRAGS * 512 + S::WAVES * 64 - 1) / (S::WAVES * 64);
-  T lval[LITERS];
-#pragma unroll
-  for (int i = 0; i < LITERS; ++i) {
-    const int e = tid + i * S::WAVES * 64;
-    const int j = e & 7, l = (e >> 3) & 63, fr = e >> 9;
-    const int mb = fr / KS2, s = fr % KS2;
-    const int m = 16 * mb + (l & 15);
-    const int mp = 32 * s + 16 * (j >> 2) + 4 * (l >> 4) + (j & 3);
-    const bool inside = e < S::LFRAGS * 512 && mp < M;
-    const T v = left[inside ? mp * M + m : 0];   // unconditional load: no branch, no serialising wait
-    lval[i] = inside ? v : DT::from_f(0.f);
-  }
-#pragma unroll
-  for (int i = 0; i < LITERS; ++i) {
-    const int e = tid + i * S::WAVES * 64;
-    if (e < S::LFRAGS * 512) lfrag[e] = lval[i];
-  }
+  issue(g, xbuf0);   // first X group in flight while L and R are set up (grid <= ngroups)
 
   // R as B-operand fragments of the first product for this wave's pair:
   // rf[h][ks][j] = R[32ks + 8lg + j][n], n = 32q + 8(li/4) + 4h + li%4.
+  // Gathered straight from global memory; all loads issue before any use.
   V rf[2][KS1];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -479,19 +483,53 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
       for (int j = 0; j < 8; ++j) rf[h][ks][j] = right[(32 * ks + 8 * lg + j) * N + n];
   }
 
-  lds_barrier();  // lfrag visible
+  // L, staged row-major through the free X stage with coalesced 16-byte
+  // copies, then gathered into B-operand fragments of the second product held
+  // in VGPRs: lf[mb][s][j] = L[m'][m], m = 16mb + li,
+  // m' = 32s + 16(j/4) + 4lg + j%4 — the row order of Z's accumulator pairs —
+  // and, for odd M/16, lt[mb][j] = L[16(MB-1) + 4lg + j][m].
+  {
+    constexpr int CHUNKS = M * M / 8;   // 16-byte chunks of L
+    typedef int v4i_t __attribute__((ext_vector_type(4)));
+    v4i_t tmp[(CHUNKS + NT - 1) / NT];
+#pragma unroll
+    for (int i = 0; i < (CHUNKS + NT - 1) / NT; ++i) {
+      const int c = tid + i * NT;
+      tmp[i] = reinterpret_cast<const v4i_t*>(left)[c < CHUNKS ? c : 0];
+    }
+#pragma unroll
+    for (int i = 0; i < (CHUNKS + NT - 1) / NT; ++i) {
+      const int c = tid + i * NT;
+      if (c < CHUNKS) reinterpret_cast<v4i_t*>(xbuf1)[c] = tmp[i];
+    }
+  }
+  lds_barrier();
+  using V4 = typename MfmaOps<DT>::V4;
+  V lf[MB][KS2 + 1];
+  V4 lt[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int s = 0; s < KS2; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) lf[mb][s][j] = xbuf1[(32 * s + 16 * (j >> 2) + 4 * lg + (j & 3)) * M + 16 * mb + li];
+    // trailing 16-deep slab: m' = 16(MB-1) + 4lg + j
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lt[mb][j] = xbuf1[(S::TAIL ? 16 * (MB - 1) + 4 * lg + j : 0) * M + 16 * mb + li];
+  }
+  lds_barrier();   // xbuf1 is free again for the first prefetch
 
   while (g < ngroups) {
     int64_t gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf1);
-    fq_mfma_group<DT, MB, NP, PACK>(xbuf0 + tau * S::XFRAGS * 512, lfrag, rf, red, g * S::TPB + tau, tokens,
-                                    clip, out_codes, out_scales, lane, tau, q);
+    fq_mfma_group<DT, MB, NP, PACK>(xbuf0 + tau * S::XFRAGS * 512, lf, lt, rf, red, g * S::TPB + tau, tokens, clip,
+                                    out_codes, out_scales, lane, tau, q);
     g = gn;
     if (g >= ngroups) break;
     gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf0);
-    fq_mfma_group<DT, MB, NP, PACK>(xbuf1 + tau * S::XFRAGS * 512, lfrag, rf, red, g * S::TPB + tau, tokens,
-                                    clip, out_codes, out_scales, lane, tau, q);
+    fq_mfma_group<DT, MB, NP, PACK>(xbuf1 + tau * S::XFRAGS * 512, lf, lt, rf, red, g * S::TPB + tau, tokens, clip,
+                                    out_codes, out_scales, lane, tau, q);
     g = gn;
   }
   wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
@@ -514,8 +552,8 @@ static int launch_mfma(const void* x, int64_t tokens, int64_t x_ld, const void* 
                        float clip, void* out_codes, float* out_scales, hipStream_t stream) {
   using S = FqShape<MB, NP>;
   using T = typename DT::T;
-  constexpr size_t lds = (S::LFRAGS + 2 * S::STAGE_FRAGS) * 64 * 8 * sizeof(T);  // static LDS of the kernel
-  const int per_cu = lds <= 80 * 1024 ? 2 : 1;
+  constexpr size_t lds = 2 * S::STAGE_ELEMS * sizeof(T);  // static LDS of the kernel
+  const int per_cu = (int)std::min<size_t>(4, (160 * 1024) / (lds + 256));
   const int64_t ngroups = (tokens + S::TPB - 1) / S::TPB;
   int64_t grid = (int64_t)device_cu_count() * per_cu;
   if (grid > ngroups) grid = ngroups;
