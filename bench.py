@@ -15,6 +15,8 @@ the wide quantize (config 3) and the end-to-end W4A4 linear (config 5).
 fallback on a bounded sample on the host cores (a reported baseline, not a target).
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-secondary] [--no-cpu]
+       python bench.py --pmc-pass                       (under rocprofv3 --pmc FETCH_SIZE or WRITE_SIZE)
+       python bench.py --pmc-summary FETCH_DIR WRITE_DIR
 """
 import argparse
 import json
@@ -216,6 +218,102 @@ def cpu_baseline_gemm(torch, budget_s=8.0):
             "sample": f"128 x 14336 x 4096 slab of config 4, median of {len(times)} runs ({med:.2f} s each)"}
 
 
+# Kernel of each benched workload, as rocprofv3 names it (a substring of the demangled name).
+KERNEL_OF = {
+    "quantize_cfg2": "fq_mfma_kernel<qo::F16T, 4, 2, true>",
+    "quantize_cfg3": "fq_mfma_kernel<qo::BF16T, 7, 4, true>",
+    "gemm_cfg4": "gemm_i4_mfma",
+}
+COPY_PROBE_BYTES = 1 << 30      # float32 negation of 1 GiB: reads and writes exactly this many bytes
+COPY_PROBE_KERNEL = "neg_kernel"
+
+
+def pmc_pass(torch, dev):
+    """Eager launches for a rocprofv3 --pmc run (one counter block per run).
+
+    Each benched kernel runs 4 times on fresh buffers, then a plain copy kernel
+    of known size (float32 negation, 1 GiB in, 1 GiB out) runs 4 times: its
+    counter readings give the scale from FETCH_SIZE / WRITE_SIZE to bytes.
+    """
+    from quant_ops_amd import capi
+    from quant_ops_amd import workloads as wl
+
+    for case in (wl.quant_cfg2(), wl.quant_cfg3()):
+        t, f = case.x.shape
+        x = case.x.to(dev)
+        L, R = case.left.to(dev), case.right.to(dev)
+        for _ in range(4):
+            xi = x.clone()
+            codes = torch.empty((t, f // 8), dtype=torch.int32, device=dev)
+            scales = torch.empty(t, dtype=torch.float32, device=dev)
+            capi.flatquant_quantize(xi, L, R, case.clip_ratio, True, out_codes=codes, out_scales=scales)
+            torch.cuda.synchronize()
+        del x, xi, codes, scales
+    case = wl.gemm_cfg4()
+    a, b = case.a.to(dev), case.b.to(dev)
+    sa, sb = case.scale_a.to(dev), case.scale_b.to(dev)
+    for _ in range(4):
+        out = torch.empty(case.mnk[:2], dtype=case.out_dtype, device=dev)
+        capi.int4_gemm(a.clone(), b.clone(), sa, sb, out=out)
+        torch.cuda.synchronize()
+    del a, b, out
+    src = torch.randn(COPY_PROBE_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+    print(json.dumps({"pmc_pass": True, "copy_probe_bytes": COPY_PROBE_BYTES, "kernels": KERNEL_OF}), flush=True)
+
+
+def pmc_summary(fetch_dir, write_dir):
+    """Per-launch HBM bytes of each benched kernel from two rocprofv3 --pmc runs.
+
+    Reads the counter_collection CSVs of a FETCH_SIZE run and a WRITE_SIZE run
+    (KiB per dispatch), takes the median over dispatches of each kernel, and
+    divides by what the same counter reads per byte for the copy probe.
+    """
+    import csv
+    import glob
+    import statistics
+
+    def per_kernel(root, counter):
+        vals = {}
+        files = glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            raise SystemExit(f"no counter_collection.csv under {root}")
+        for path in files:
+            with open(path, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    if row.get("Counter_Name") != counter:
+                        continue
+                    vals.setdefault((row["Kernel_Name"], row["Dispatch_Id"]), 0.0)
+                    vals[(row["Kernel_Name"], row["Dispatch_Id"])] += float(row["Counter_Value"])
+        by_name = {}
+        for (name, _), v in vals.items():
+            by_name.setdefault(name, []).append(v)
+        return by_name
+
+    def pick(by_name, key):
+        hits = [v for name, v in by_name.items() if key in name]
+        if not hits:
+            return None
+        return statistics.median([x for v in hits for x in v]) * 1024.0   # KiB -> bytes
+
+    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    f_copy, w_copy = pick(fetch, COPY_PROBE_KERNEL), pick(write, COPY_PROBE_KERNEL)
+    if not f_copy or not w_copy:
+        raise SystemExit("copy probe kernel not found in the counter files")
+    ff, wf = f_copy / COPY_PROBE_BYTES, w_copy / COPY_PROBE_BYTES
+    out = {"copy_probe": {"bytes": COPY_PROBE_BYTES, "fetch_factor": ff, "write_factor": wf}}
+    for key, kname in KERNEL_OF.items():
+        fb, wb = pick(fetch, kname), pick(write, kname)
+        if fb is None or wb is None:
+            continue
+        out[key] = {"kernel": kname, "fetch_bytes_raw": fb, "write_bytes_raw": wb,
+                    "fetch_bytes": fb / ff, "write_bytes": wb / wf, "hbm_bytes_per_launch": fb / ff + wb / wf}
+    print(json.dumps(out, indent=1))
+
+
 def _traffic_from_profiles(kernel_key):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE), if committed."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -235,7 +333,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-secondary", action="store_true", help="only the primary workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="eager launches of each benched kernel and a copy probe, for rocprofv3 --pmc")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print per-launch HBM bytes from two rocprofv3 --pmc output folders")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the hot path shards over tokens with no "
               f"communication); --gpus {args.gpus} is not supported", file=sys.stderr)
@@ -257,6 +362,9 @@ def main():
         print(f"bench.py: HIP library not loaded: {qo._loader.LOAD_ERROR}", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda", 0)
+    if args.pmc_pass:
+        pmc_pass(torch, dev)
+        return
 
     _log("primary: config 2 quantize")
     primary = bench_quant(torch, wl.quant_cfg2(), args.steps, args.warmup, dev)

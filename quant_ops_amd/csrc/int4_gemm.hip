@@ -6,9 +6,10 @@
 // int4_matmul_pytorch (int4_matmul/ops.py:69-103): the float32 matmul of
 // integers is exact, then two separate float32 products, then one rounding.
 //
-// Fast kernel (gemm_i4_mfma): gfx950 has no int4 MFMA, so nibbles are widened
-// to int8 on the way from registers into LDS and fed to
-// v_mfma_i32_16x16x64_i8. Widening trick: XOR with 0x8 turns the offset code
+// MFMA kernels: gfx950 has no int4 MFMA, so nibbles are widened to int8 and
+// fed to v_mfma_i32_16x16x64_i8. gemm_i4_dma (K % 128 == 0, the main path)
+// stages packed words in LDS and widens after the LDS read; gemm_i4_mfma
+// (any K % 8 == 0) widens on the way from registers into LDS. Widening trick: XOR with 0x8 turns the offset code
 // (q + 8) into q's 4-bit two's-complement pattern; placing it in the high half
 // of a byte gives the int8 value 16*q. Both operands carry the factor 16, so the
 // accumulator holds 256*acc, exact while 256 * 64 * K < 2^31 (K <= 65536); the
@@ -18,6 +19,8 @@
 // Generic kernel (gemm_i4_generic): one output per thread, any strides and
 // sizes (K < 2^21). Used when the fast kernel's layout / alignment
 // requirements are not met.
+#include <type_traits>
+
 #include "common.h"
 
 #ifndef QO_GEMM_TILE
@@ -284,8 +287,289 @@ gemm_i4_mfma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restri
 }
 
 // ---------------------------------------------------------------------------
+// Pipelined MFMA kernel (gemm_i4_dma): packed words go from global memory to
+// LDS by LDS-DMA (global_load_lds_dwordx4, no VGPR staging) through a ring of
+// STAGES buffers, 128 k (16 packed words per row) per stage; nibbles are
+// widened to int8 in registers after the LDS read, so LDS holds and serves
+// half the bytes of a widened layout.
+//
+// Operand layout. A lane's 16-byte DMA chunk is four consecutive packed words
+// of one row (A) or column (B): lane L of chunk c holds row 16c + L%16, words
+// 4(L/16) .. 4(L/16)+3 of the stage. Those four words feed two MFMAs: words
+// 4g, 4g+1 the first (h = 0) and 4g+2, 4g+3 the second (h = 1), g = L/16, each
+// word widened to a "low" and a "high" dword. A and B follow the same word
+// order, which is all the MFMA needs (k order is free if both operands agree).
+//
+// B layouts:
+//  * NK (b_stride_p == 1, the W.t() view): B chunks exactly like A's.
+//  * KN (b_stride_n == 1, the reference's [K/8, N]): the DMA copies rows of
+//    packed words (256 columns per 1 KiB DMA) into LDS rows of KN_ROW bytes,
+//    and a lane reads its four words with four ds_read_b32 (rows 4g .. 4g+3,
+//    its column). KN_ROW = 1040 puts the four lane groups on distinct banks.
+// ---------------------------------------------------------------------------
+
+template <int BM, int BN, bool B_NK>
+struct DmaStage {
+  static constexpr int A_BYTES = BM / 16 * 1024;
+  static constexpr int KN_ROW = 1040;
+  static constexpr int B_BYTES = B_NK ? BN / 16 * 1024 : 16 * KN_ROW;
+  static constexpr int BYTES = A_BYTES + B_BYTES;
+  static constexpr int A_DMA = BM / 16;
+  static constexpr int B_DMA = B_NK ? BN / 16 : 16;
+  static constexpr int DMA = A_DMA + B_DMA;
+  static_assert(BM % 16 == 0 && BN % 16 == 0, "tile");
+  static_assert(B_NK || BN <= 256, "a KN row of the tile must fit one 1 KiB DMA");
+};
+
+// LDS-DMA of 16 bytes per lane: lane l's bytes land at LDS address lds + 16 l
+// (lds is wave-uniform, passed in M0). Issued as inline assembly so the
+// compiler's wait insertion does not see an LDS write it cannot order: with
+// the builtin it falls back to waiting for every outstanding load before LDS
+// reads at control-flow joins. The kernel orders these copies itself with
+// explicit vmcnt waits and barriers; every other load stays visible to the
+// compiler, and its own vmcnt waits remain correct (extra outstanding loads
+// only make them stricter).
+__device__ inline void dma16(const void* src, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+template <int N>
+__device__ inline void gemm_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// widen16 in the form gfx950's three-input v_bitop3_b32 takes in one
+// instruction per dword (plus the shift): (w << 4) ^ (0x88888888 << 4) and
+// w ^ 0x88888888, each masked to the high nibbles.
+__device__ inline void widen16_b3(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  lo = ((w << 4) ^ 0x88888880u) & 0xF0F0F0F0u;
+  hi = (w ^ 0x88888888u) & 0xF0F0F0F0u;
+}
+
+// Two packed words -> one 16-byte MFMA operand (low, high dword of each).
+__device__ inline v4i widen_pair(int w0, int w1) {
+  uint32_t l0, h0, l1, h1;
+  widen16_b3((uint32_t)w0, l0, h0);
+  widen16_b3((uint32_t)w1, l1, h1);
+  return v4i{(int)l0, (int)h0, (int)l1, (int)h1};
+}
+
+// Scale element i of a float32 / float16 / bfloat16 vector (dtype fixed at
+// compile time).
+template <int DT>
+__device__ inline float scale_at(const void* p, int64_t i) {
+  if constexpr (DT == QO_DTYPE_F32) return reinterpret_cast<const float*>(p)[i];
+  else if constexpr (DT == QO_DTYPE_F16) return (float)reinterpret_cast<const _Float16*>(p)[i];
+  else return (float)reinterpret_cast<const __bf16*>(p)[i];
+}
+
+// Calls f(std::integral_constant<int, dtype>) for a runtime scale dtype code.
+template <class F>
+__device__ inline void with_scale_dtype(int code, F&& f) {
+  if (code == QO_DTYPE_F32) f(std::integral_constant<int, QO_DTYPE_F32>{});
+  else if (code == QO_DTYPE_F16) f(std::integral_constant<int, QO_DTYPE_F16>{});
+  else f(std::integral_constant<int, QO_DTYPE_BF16>{});
+}
+
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool B_NK, class OT>
+__global__ void __launch_bounds__(64 * WGM * WGN, 1)
+gemm_i4_dma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
+            const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
+            typename OT::T* __restrict__ out, int64_t ldc, int M, int N, int K, int tiles_m) {
+  using S = DmaStage<BM, BN, B_NK>;
+  constexpr int W = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int FM = WM / 16, FN = WN / 16;
+  constexpr int PER = (S::DMA + W - 1) / W;   // DMA instructions per wave per stage
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile");
+  static_assert(STAGES >= 2 && STAGES <= 4, "stages");
+  static_assert(PER * (STAGES - 2) < 64, "vmcnt range");
+
+  // One LDS object per stage: the compiler can then tell a read of one stage
+  // from the DMA still writing another, and waits only for the right one.
+  __shared__ __align__(16) unsigned char st0[S::BYTES];
+  __shared__ __align__(16) unsigned char st1[S::BYTES];
+  __shared__ __align__(16) unsigned char st2[STAGES > 2 ? S::BYTES : 16];
+  __shared__ __align__(16) unsigned char st3[STAGES > 3 ? S::BYTES : 16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int li = lane & 15, lg = lane >> 4;
+
+  // XCD-aware tile order (see gemm_i4_mfma).
+  const int nblk = gridDim.x;
+  int pid = blockIdx.x;
+  if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
+  const int tm = pid % tiles_m, tn = pid / tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = K >> 7;                       // stages of 128 k (K % 128 == 0)
+
+  // Source addresses of this wave's DMA instructions at stage 0 (clamped rows
+  // and columns only feed accumulators that are never stored); stage t adds
+  // 16 t words (A, NK) or 16 t rows (KN).
+  const int32_t* src[PER];
+  uint32_t dst[PER];   // wave-uniform LDS offsets inside a stage
+  int64_t step[PER];
+#pragma unroll
+  for (int t = 0; t < PER; ++t) {
+    int i = __builtin_amdgcn_readfirstlane(wave) + W * t;
+    i = i < S::DMA ? i : S::DMA - 1;           // spare slots repeat the last copy (same bytes, same place)
+    if (i < S::A_DMA) {
+      const int m = min(m0 + 16 * i + li, M - 1);
+      src[t] = a + (int64_t)m * lda + 4 * lg;
+      dst[t] = i * 1024;
+      step[t] = 16;
+    } else if (B_NK) {
+      const int c = i - S::A_DMA;
+      const int n = min(n0 + 16 * c + li, N - 1);
+      src[t] = b + (int64_t)n * ldb + 4 * lg;
+      dst[t] = S::A_BYTES + c * 1024;
+      step[t] = 16;
+    } else {
+      const int p = i - S::A_DMA;
+      const int n = min(n0 + 4 * lane, N - 4);
+      src[t] = b + (int64_t)p * ldb + n;
+      dst[t] = S::A_BYTES + p * S::KN_ROW;
+      step[t] = 16 * ldb;
+    }
+  }
+
+  auto stage_ptr = [&](auto buf) -> unsigned char* {
+    constexpr int J = decltype(buf)::value;
+    if constexpr (J == 0) return st0;
+    else if constexpr (J == 1) return st1;
+    else if constexpr (J == 2) return st2;
+    else return st3;
+  };
+  auto issue = [&](int ks, auto buf) {
+    const uint32_t base =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)stage_ptr(buf);
+#pragma unroll
+    for (int t = 0; t < PER; ++t) dma16(src[t] + ks * step[t], base + dst[t]);
+  };
+
+  v4i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  auto compute = [&](auto buf) {
+    const unsigned char* base = stage_ptr(buf);
+    v4i ar[FM], br[FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) ar[i] = *reinterpret_cast<const v4i*>(base + (wm * FM + i) * 1024 + 16 * lane);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (B_NK) {
+        br[j] = *reinterpret_cast<const v4i*>(base + S::A_BYTES + (wn * FN + j) * 1024 + 16 * lane);
+      } else {
+        const unsigned char* col = base + S::A_BYTES + (wn * WN + 16 * j + li) * 4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) br[j][t] = *reinterpret_cast<const int*>(col + (4 * lg + t) * S::KN_ROW);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4i fa[FM];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) fa[i] = widen_pair(ar[i][2 * h], ar[i][2 * h + 1]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const v4i fb = widen_pair(br[j][2 * h], br[j][2 * h + 1]);
+        // transposed product: acc[i][j] holds C[16i + lane%16][16j + 4(lane/16) + r]
+#pragma unroll
+        for (int i = 0; i < FM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, fa[i], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // Step for stage s held in buffer J = s % STAGES: wait for this wave's DMA
+  // of stage s, barrier (every wave's part has landed and every wave is done
+  // with stage s - 1), refill stage s - 1's buffer with stage s + STAGES - 1,
+  // then the MFMAs of stage s. Past the last stage the refill re-reads stage
+  // nk - 1 into the free buffer, so every step issues the same loads and the
+  // wait count is a constant (a conditional refill makes the compiler wait for
+  // all outstanding loads before the LDS reads that follow it).
+  auto step_stage = [&](int s, auto buf) {
+    constexpr int J = decltype(buf)::value;
+    gemm_wait_vmcnt<PER * (STAGES - 2)>();
+    // lgkmcnt(0): this wave's reads of stage s - 1 have returned before any
+    // wave passes the barrier and refills that buffer
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(min(s + STAGES - 1, nk - 1), std::integral_constant<int, (J + STAGES - 1) % STAGES>{});
+    compute(buf);
+  };
+
+  issue(0, std::integral_constant<int, 0>{});
+  if constexpr (STAGES > 2) issue(min(1, nk - 1), std::integral_constant<int, 1>{});
+  if constexpr (STAGES > 3) issue(min(2, nk - 1), std::integral_constant<int, 2>{});
+  for (int s = 0; s < nk; s += STAGES) {
+    step_stage(s, std::integral_constant<int, 0>{});
+    if (s + 1 < nk) step_stage(s + 1, std::integral_constant<int, 1>{});
+    if constexpr (STAGES > 2)
+      if (s + 2 < nk) step_stage(s + 2, std::integral_constant<int, 2>{});
+    if constexpr (STAGES > 3)
+      if (s + 3 < nk) step_stage(s + 3, std::integral_constant<int, 3>{});
+  }
+  gemm_wait_vmcnt<0>();
+
+  // Epilogue: undo the 256x scale, two float32 products, one rounding.
+  using T = typename OT::T;
+  float sav[FM], sbv[FN][4];
+  with_scale_dtype(sad, [&](auto dt) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) sav[i] = scale_at<decltype(dt)::value>(sa, min(m0 + wm * WM + 16 * i + li, M - 1));
+  });
+  with_scale_dtype(sbd, [&](auto dt) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sbv[j][r] = scale_at<decltype(dt)::value>(sb, min(n0 + wn * WN + 16 * j + 4 * lg + r, N - 1));
+  });
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * WM + 16 * i + li;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WN + 16 * j + 4 * lg;
+      if (n >= N) continue;
+      T v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(acc[i][j][r] >> 8, sav[i], sbv[j][r]));
+      T* o = out + (int64_t)m * ldc + n;
+      if (n + 3 < N) {
+        if constexpr (sizeof(T) == 2) {
+          typedef short v4s __attribute__((ext_vector_type(4)));
+          v4s pk;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
+          *reinterpret_cast<v4s*>(o) = pk;
+        } else {
+          *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) o[r] = v[r];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host dispatch.
 // ---------------------------------------------------------------------------
+
+// QO_GEMM_NO_DMA=1 keeps the register-staged MFMA kernel for every shape
+// (tests use it to cross-check the two MFMA kernels).
+static bool gemm_allow_dma() {
+  const char* e = getenv("QO_GEMM_NO_DMA");
+  return !(e && e[0] == '1');
+}
 
 template <class OT>
 static void launch_generic(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, int64_t bsn,
@@ -306,6 +590,54 @@ static void launch_mfma(const int32_t* a, int64_t lda, const int32_t* b, int64_t
                      tiles_n);
 }
 
+#ifndef QO_GEMM_DMA_WAVES
+#define QO_GEMM_DMA_WAVES 4, 2
+#endif
+#ifndef QO_GEMM_DMA_STAGES
+#define QO_GEMM_DMA_STAGES 4
+#endif
+
+template <int BM, int BN, bool B_NK, class OT>
+static void launch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
+                       const void* sb, int sbd, void* out, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  constexpr int WGM_WGN[2] = {QO_GEMM_DMA_WAVES};
+  hipLaunchKernelGGL((gemm_i4_dma<BM, BN, WGM_WGN[0], WGM_WGN[1], QO_GEMM_DMA_STAGES, B_NK, OT>),
+                     dim3(tiles_m * tiles_n), dim3(64 * WGM_WGN[0] * WGM_WGN[1]), 0, stream, a, lda, b, ldb, sa,
+                     sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, M, N, K, tiles_m);
+}
+
+// Fraction of the machine's workgroup slots doing useful output in a launch
+// of BM x BN tiles (one workgroup per CU): tile-count rounding plus ragged
+// edge tiles.
+static double tile_efficiency(int64_t M, int64_t N, int BM, int BN, int cus) {
+  const int64_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  const int64_t tiles = tm * tn, rounds = (tiles + cus - 1) / cus;
+  return (double)(M * N) / ((double)rounds * cus * BM * BN);
+}
+
+static int gemm_cu_count() {
+  static int cached = 0;
+  if (cached) return cached;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+    cached = cus;
+  else
+    cached = 256;
+  return cached;
+}
+
+template <bool B_NK, class OT>
+static void dispatch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
+                         const void* sb, int sbd, void* out, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+  const int cus = gemm_cu_count();
+  if (tile_efficiency(M, N, 256, 224, cus) > tile_efficiency(M, N, 256, 256, cus))
+    launch_dma<256, 224, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, M, N, K, stream);
+  else
+    launch_dma<256, 256, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, M, N, K, stream);
+}
+
 template <class OT>
 static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, int64_t bsn, const void* sa,
                      int sad, const void* sb, int sbd, void* out, int64_t ldc, int64_t M, int64_t N, int64_t K,
@@ -319,6 +651,14 @@ static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bs
                        ((uintptr_t)out % (4 * sizeof(T)) == 0) && (ldc % 4 == 0);
   if (allow_fast && fits && aligned && (b_nk || b_kn)) {
     const int m = (int)M, n = (int)N, k = (int)K;
+    // pipelined kernel: whole 128-deep stages; KN rows read as 16-byte column groups
+    if (k % 128 == 0 && k > 0 && (b_nk || n % 4 == 0) && gemm_allow_dma()) {
+      if (b_nk)
+        dispatch_dma<true, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, m, n, k, stream);
+      else
+        dispatch_dma<false, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, m, n, k, stream);
+      return;
+    }
     if (b_nk)
       launch_mfma<QO_GEMM_TILE, true, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, m, n, k, stream);
     else

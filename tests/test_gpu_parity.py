@@ -280,6 +280,28 @@ def test_gemm_small_bit_exact(gpu, m, n, k, bview):
     assert torch.equal(out.cpu(), ref)
 
 
+# Shapes for the pipelined kernel (K % 128 == 0): ragged M / N edges, one and
+# several tile sizes, both B layouts; cross-checked against the oracle and the
+# register-staged kernel.
+@pytest.mark.parametrize("m,n,k", [(1, 4, 128), (16, 16, 128), (300, 260, 1024), (257, 516, 2048),
+                                   (512, 448, 512), (256, 224, 384), (33, 12, 256), (1024, 1792, 1152)])
+@pytest.mark.parametrize("bview", [False, True])
+def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, monkeypatch):
+    case = wl.gemm_case(m, n, k, seed=3 * m + n + k, b_transposed_view=bview)
+    _say(f"gemm dma {m}x{n}x{k} bview={bview}")
+    a, b = case.a.to(gpu), case.b.to(gpu)
+    one_a, one_b = torch.ones(m, device=gpu), torch.ones(n, device=gpu)
+    acc = capi.int4_gemm(a, b, one_a, one_b, out_dtype=torch.float32)
+    out = capi.int4_gemm(a, b, case.scale_a.to(gpu), case.scale_b.to(gpu))
+    monkeypatch.setenv("QO_GEMM_NO_DMA", "1")
+    out_old = capi.int4_gemm(a, b, case.scale_a.to(gpu), case.scale_b.to(gpu))
+    monkeypatch.delenv("QO_GEMM_NO_DMA")
+    torch.cuda.synchronize()
+    assert torch.equal(acc.cpu().to(torch.int64), _gemm_ref_acc(case.a, case.b).to(torch.int64))
+    assert torch.equal(out.cpu(), oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b))
+    assert torch.equal(out, out_old)
+
+
 @pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
 def test_gemm_scale_and_out_dtypes(gpu, sdt, odt):
