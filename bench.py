@@ -17,6 +17,7 @@ fallback on a bounded sample on the host cores (a reported baseline, not a targe
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-secondary] [--no-cpu]
        python bench.py --pmc-pass                       (under rocprofv3 --pmc FETCH_SIZE or WRITE_SIZE)
        python bench.py --pmc-summary FETCH_DIR WRITE_DIR
+       python bench.py --trace-summary KERNEL_TRACE_CSV    (rocprofv3 --kernel-trace --output-format csv)
 """
 import argparse
 import json
@@ -222,7 +223,7 @@ def cpu_baseline_gemm(torch, budget_s=8.0):
 KERNEL_OF = {
     "quantize_cfg2": "fq_mfma_kernel<qo::F16T, 4, 2, true>",
     "quantize_cfg3": "fq_mfma_kernel<qo::BF16T, 7, 4, true>",
-    "gemm_cfg4": "gemm_i4_mfma",
+    "gemm_cfg4": "gemm_i4_dma<256, 224, 4, 2, 4, false, qo::OutF16>",
 }
 COPY_PROBE_BYTES = 1 << 30      # float32 negation of 1 GiB: reads and writes exactly this many bytes
 COPY_PROBE_KERNEL = "neg_kernel"
@@ -314,6 +315,56 @@ def pmc_summary(fetch_dir, write_dir):
     print(json.dumps(out, indent=1))
 
 
+# Workloads in the order the default bench run dispatches them (one segment of
+# launches each; the config 5 linear interleaves its two kernels).
+BENCH_SEGMENTS = [
+    ("quantize cfg2", 20996096, None), ("gemm cfg4", None, 481036337152), ("quantize cfg3", 293691904, None),
+    ("cfg5 T=16 quantize", 16 * 14336 * 2 + 16 * 1792 * 4 + 16 * 4 + 2 * (112 * 112 + 128 * 128), None),
+    ("cfg5 T=16 gemm", None, 2 * 16 * 4096 * 14336),
+    ("cfg5 T=4096 quantize", 4096 * 14336 * 2 + 4096 * 1792 * 4 + 4096 * 4 + 2 * (112 * 112 + 128 * 128), None),
+    ("cfg5 T=4096 gemm", None, 2 * 4096 * 4096 * 14336),
+]
+
+
+def trace_summary(trace_csv):
+    """Per-workload kernel durations from a rocprofv3 --kernel-trace CSV of a default bench run.
+
+    Dispatches of this library's kernels are split into segments (a new segment
+    starts when a kernel reappears after more than 16 other dispatches) and the
+    segments, in dispatch order, are matched to BENCH_SEGMENTS.
+    """
+    import csv
+    import statistics
+
+    rows = [r for r in csv.DictReader(open(trace_csv)) if "qo::" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    segs, last = [], {}
+    for r in rows:
+        key = (r["Kernel_Name"], r["Grid_Size_X"], r["Workgroup_Size_X"])
+        did = int(r["Dispatch_Id"])
+        if key not in last or did - last[key][0] > 16:
+            seg = {"key": key, "first": did, "dur": []}
+            segs.append(seg)
+            last[key] = (did, seg)
+        seg = last[key][1]
+        last[key] = (did, seg)
+        seg["dur"].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    segs.sort(key=lambda s: s["first"])
+    labelled = len(segs) == len(BENCH_SEGMENTS)
+    lines = [f"{'workload':22s} {'calls':>5s} {'avg_us':>9s} {'median_us':>9s} {'min_us':>9s} {'max_us':>9s} "
+             f"{'GB/s':>7s} {'TOP/s':>7s}  kernel [grid x block]"]
+    for i, s in enumerate(segs):
+        d = s["dur"]
+        avg = sum(d) / len(d) / 1e3
+        name, nbytes, ops = BENCH_SEGMENTS[i] if labelled else (f"segment {i}", None, None)
+        gbs = f"{nbytes / avg / 1e3:7.0f}" if nbytes else f"{'':7s}"
+        tops = f"{ops / avg / 1e6:7.0f}" if ops else f"{'':7s}"
+        kname = s["key"][0].split("(")[0].replace("void ", "")
+        lines.append(f"{name:22s} {len(d):5d} {avg:9.2f} {statistics.median(d) / 1e3:9.2f} {min(d) / 1e3:9.2f} "
+                     f"{max(d) / 1e3:9.2f} {gbs} {tops}  {kname} [{s['key'][1]} x {s['key'][2]}]")
+    print("\n".join(lines))
+
+
 def _traffic_from_profiles(kernel_key):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE), if committed."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -335,11 +386,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="eager launches of each benched kernel and a copy probe, for rocprofv3 --pmc")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="per-workload kernel durations from a rocprofv3 kernel trace of a default run")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print per-launch HBM bytes from two rocprofv3 --pmc output folders")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the hot path shards over tokens with no "
