@@ -38,6 +38,9 @@ HIP_FLAGS = [
     "-ffp-contract=off",
     # packed fp32 VALU forms are kept out of every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the AGPR form costs a v_accvgpr_read per result
+    # element that the epilogues consume
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-command-line-argument",
     f"-I{INCLUDE}",
 ]

@@ -74,6 +74,48 @@ __device__ inline float wave_min(float v) {
   return v;
 }
 
+// Running maximum of |v| over pairs of 16-bit floats (fp16 or bf16) packed in
+// a dword: with the sign bits cleared, their bit patterns order like the
+// values, so one packed unsigned 16-bit max handles both halves.
+__device__ inline uint32_t pk_absmax16(uint32_t m, uint32_t pair) {
+  typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+  const v2u16 a = __builtin_bit_cast(v2u16, pair & 0x7FFF7FFFu);
+  const v2u16 b = __builtin_bit_cast(v2u16, m);
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+
+// Wave-wide (64 lanes) maximum of unsigned values: DPP within each row of 16
+// lanes, then the four row results through scalar reads. Every lane receives
+// the result.
+__device__ inline uint32_t wave_max_u32(uint32_t u) {
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x140, 0xF, 0xF, false));  // row_mirror
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)u, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)u, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)u, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)u, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
+// float(low / high half of p as fp16) * r: the exact product rounded once to
+// float32, which is what converting and then multiplying gives, in one
+// v_fma_mix_f32 (with a zero addend; only the sign of a zero product can
+// differ, and no caller distinguishes it). p must not come straight from an
+// MFMA: the wait states an MFMA result needs before a VALU read are not
+// relied on around inline assembly.
+__device__ inline float mul_f16lo(uint32_t p, float r) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(p), "v"(r));
+  return d;
+}
+__device__ inline float mul_f16hi(uint32_t p, float r) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(p), "v"(r));
+  return d;
+}
+
 }  // namespace qo
 
 // Thread-local error message used by qo_last_error().

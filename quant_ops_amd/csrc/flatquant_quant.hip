@@ -42,6 +42,16 @@ __device__ inline float fq_scale(float ymax_raw, float ymin_raw, float clip) {
   return fmaxf(s, DT::round(1e-8f));
 }
 
+// The same scale from max |Y| of the D-rounded Y, valid for clip > 0:
+// rounding to nearest even is sign-symmetric and monotonic, so
+// max(|rnd(rnd(min) c)|, rnd(rnd(max) c)) = rnd(max |rnd(y)| c).
+template <class DT>
+__device__ inline float fq_scale_abs(float amax, float clip) {
+  const float bound = DT::round(amax * clip);
+  const float s = DT::round(opaque(bound) / 7.0f);
+  return fmaxf(s, DT::round(1e-8f));
+}
+
 // Code of one element from its D-rounded quotient t = rnd_D(y / s):
 // clamp(round_half_even(t), -8, 7) (ops.py:117). A NaN quotient (0/0 when an
 // fp16 token's scale rounds to 0) becomes 0 through the reference's int8 cast
@@ -209,8 +219,8 @@ struct FqEpi<F16T> {
   // fp16: 1544 = 1536 + 8 has a unit ulp, so t + 1544 is the integer 1536 + q + 8,
   // bits 0x6600 + (q + 8); both halves are handled by one v_pk_add_f16.
   __device__ static inline void accumulate(uint32_t& word, uint32_t p, float rcp, int r) {
-    const float a0 = __builtin_amdgcn_fmed3f(lo(p) * rcp, -8.0f, 7.0f);
-    const float a1 = __builtin_amdgcn_fmed3f(hi(p) * rcp, -8.0f, 7.0f);
+    const float a0 = __builtin_amdgcn_fmed3f(mul_f16lo(p, rcp), -8.0f, 7.0f);
+    const float a1 = __builtin_amdgcn_fmed3f(mul_f16hi(p, rcp), -8.0f, 7.0f);
     v2h t = __builtin_bit_cast(v2h, pack(a0, a1));
     const v2h magic = {(_Float16)1544.0f, (_Float16)1544.0f};
     t = t + magic;
@@ -536,6 +546,307 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 }
 
 // ---------------------------------------------------------------------------
+// Wave-per-token kernel (fq_wave_kernel): M = 16*MB with MB even, N = 32*NQ,
+// small enough that one wavefront holds a whole token (M = N = 64 at most).
+//
+// * X arrives by direct 16-byte loads straight into A-operand fragments: lane
+//   (li, lg) loads X[16rb + li][32ks + 8lg .. +7], each element once.
+// * L and R fragments are built once per workgroup by the matrix core. The
+//   fragments need columns of L and R (8 consecutive rows of one column per
+//   lane), while memory holds rows; an MFMA whose B operand is a one-hot
+//   selection matrix turns a row-major 16 x 32 tile (coalesced 16-byte loads)
+//   into that order: D[4lg + r][li] = A[4lg + r][sel(li)], exact, since every
+//   output is one product with 1.0 plus zeros. The waves split the build,
+//   exchange the fragments through LDS (one barrier) and keep them in VGPRs.
+// * The column permutation and the transposed second product are those of
+//   fq_mfma_kernel, so each lane ends with the 8 features of one packed word.
+// * The scale needs only an in-wave reduction.
+//
+// Waves loop over tokens (stride = all waves of the grid); the next token's X
+// is loaded into the fragment registers as soon as the first product has
+// consumed them. The scale comes from max |Y| (fq_scale_abs), so the host
+// routes clip <= 0 elsewhere.
+// ---------------------------------------------------------------------------
+
+template <class DT>
+struct DBits;
+template <>
+struct DBits<F16T> {
+  static constexpr uint32_t one = 0x3C00u;
+};
+template <>
+struct DBits<BF16T> {
+  static constexpr uint32_t one = 0x3F80u;
+};
+
+// B operand of the 16x16x32 MFMA selecting A column src for output column li:
+// lane (li, lg) holds B[8lg + j][li] = (8lg + j == src) for j = 0..7.
+template <class DT>
+__device__ inline typename MfmaOps<DT>::V onehot_b(int src, int lg) {
+  const int j = src - 8 * lg;   // the lane's slot holding the one, if 0 <= j < 8
+  const uint32_t bits = DBits<DT>::one << (16 * (j & 1));
+  v4i w;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) w[d] = ((unsigned)j < 8u && (j >> 1) == d) ? (int)bits : 0;
+  return __builtin_bit_cast(typename MfmaOps<DT>::V, w);
+}
+
+// Two selection products of the rows tiles a0 (slots j = 0..3) and a1 (slots
+// j = 4..7) assembled into one 8-element fragment (values are exact in D).
+template <class DT>
+__device__ inline typename MfmaOps<DT>::V transpose_frag(typename MfmaOps<DT>::V a0, typename MfmaOps<DT>::V a1,
+                                                        typename MfmaOps<DT>::V sel) {
+  const v4f z = {0.f, 0.f, 0.f, 0.f};
+  const v4f d0 = MfmaOps<DT>::mfma(a0, sel, z);
+  const v4f d1 = MfmaOps<DT>::mfma(a1, sel, z);
+  const v4i w = {(int)FqEpi<DT>::pack(d0[0], d0[1]), (int)FqEpi<DT>::pack(d0[2], d0[3]),
+                 (int)FqEpi<DT>::pack(d1[0], d1[1]), (int)FqEpi<DT>::pack(d1[2], d1[3])};
+  return __builtin_bit_cast(typename MfmaOps<DT>::V, w);
+}
+
+template <class DT, int MB, int NQ>
+__device__ inline void fq_wave_load_x(const typename DT::T* __restrict__ xt,
+                                      typename MfmaOps<DT>::V (&xf)[MB][NQ], int li, int lg) {
+  constexpr int N = 32 * NQ;
+#pragma unroll
+  for (int rb = 0; rb < MB; ++rb)
+#pragma unroll
+    for (int ks = 0; ks < NQ; ++ks)
+      xf[rb][ks] = *reinterpret_cast<const typename MfmaOps<DT>::V*>(xt + (16 * rb + li) * N + 32 * ks + 8 * lg);
+}
+
+// Transform fragments: R's rf[q][h][ks] at index (2q + h) KS1 + ks, then L's
+// lf[mb][s] at 2 NQ KS1 + mb KS2 + s; one 1 KiB fragment per index (16 bytes
+// per lane). A build job is one pair of row tiles and the two fragments its
+// selection products give: R job (q, ks) -> rf[q][0..1][ks], L job (s, p) ->
+// lf[2p..2p+1][s].
+template <int MB, int NQ>
+struct WaveFrags {
+  static constexpr int KS1 = NQ, KS2 = MB / 2;
+  static constexpr int NR = 2 * NQ * KS1;
+  static constexpr int NF = NR + MB * KS2;
+  static constexpr int JR = NQ * KS1;            // R jobs
+  static constexpr int NJ = JR + KS2 * (MB / 2); // all jobs
+};
+
+constexpr int kWaveKernelWaves = 8;
+
+template <class DT, int MB, int NQ, bool PACK>
+__global__ void __launch_bounds__(64 * kWaveKernelWaves)
+fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+               const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
+               void* __restrict__ out_codes, float* __restrict__ out_scales) {
+  static_assert(MB % 2 == 0 && MB >= 2 && NQ >= 1, "shape");
+  using T = typename DT::T;
+  using Ops = MfmaOps<DT>;
+  using V = typename Ops::V;
+  using Epi = FqEpi<DT>;
+  using W = WaveFrags<MB, NQ>;
+  constexpr int NW = kWaveKernelWaves;
+  constexpr int M = 16 * MB, N = 32 * NQ, F = M * N;
+  constexpr int KS1 = W::KS1;    // 32-deep slabs of the first product (k = n')
+  constexpr int KS2 = W::KS2;    // 32-deep slabs of the second product (k = m')
+  constexpr int JPW = (W::NJ + NW - 1) / NW;
+  __shared__ __align__(16) unsigned char frag_lds[W::NF * 1024];
+
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15, lg = lane >> 4;
+  const int wave = threadIdx.x >> 6;
+  const int64_t nwaves = (int64_t)gridDim.x * NW;
+  int64_t t = (int64_t)blockIdx.x * NW + wave;
+
+  // Row tiles of this wave's build jobs first, then the first token's X: the
+  // fragment build below waits only for the tiles (loads retire in order)
+  // while X is still in flight. No branches around these loads (a branch
+  // would make the compiler's wait counts conservative): a wave without a job
+  // repeats the last one and writes the same bytes to the same place, a wave
+  // without a token loads the last token and stores nothing.
+  //   R job (q, ks): A_e[i][k] = R[32ks + 8(i/4) + i%4 + 4e][32q + k]
+  //   L job (s, p):  A_e[i][k] = L[32s + 16e + i][32p + k]
+  V ja[JPW][2];
+#pragma unroll
+  for (int i = 0; i < JPW; ++i) {
+    const int j = min(wave + i * NW, W::NJ - 1);
+    {
+      const T* base;
+      int off1;
+      if (j < W::JR) {
+        const int q = j / KS1, ks = j % KS1;
+        base = right + (32 * ks + 8 * (li >> 2) + (li & 3)) * N + 32 * q + 8 * lg;
+        off1 = 4 * N;
+      } else {
+        const int s = (j - W::JR) / (MB / 2), p = (j - W::JR) % (MB / 2);
+        base = left + (32 * s + li) * M + 32 * p + 8 * lg;
+        off1 = 16 * M;
+      }
+      ja[i][0] = *reinterpret_cast<const V*>(base);
+      ja[i][1] = *reinterpret_cast<const V*>(base + off1);
+    }
+  }
+  V xf[MB][KS1];
+  fq_wave_load_x<DT, MB, NQ>(x + min(t, tokens - 1) * x_ld, xf, li, lg);
+
+  // Build: selection sel_h(li) = 8(li/4) + 4h + li%4 gives R's permuted pair
+  // columns, sel_c(li) = 16c + li the two 16-column halves of an L tile:
+  //   rf[q][h][ks][j] = R[32ks + 8lg + j][32q + 8(li/4) + 4h + li%4]
+  //   lf[mb][s][j]    = L[32s + 16(j/4) + 4lg + j%4][16mb + li]
+#pragma unroll
+  for (int i = 0; i < JPW; ++i) {
+    const int j = min(wave + i * NW, W::NJ - 1);
+    {
+      int f0, f1, src0, src1;
+      if (j < W::JR) {
+        const int q = j / KS1, ks = j % KS1;
+        f0 = (2 * q) * KS1 + ks;
+        f1 = (2 * q + 1) * KS1 + ks;
+        src0 = 8 * (li >> 2) + (li & 3);
+        src1 = src0 + 4;
+      } else {
+        const int s = (j - W::JR) / (MB / 2), p = (j - W::JR) % (MB / 2);
+        f0 = W::NR + (2 * p) * KS2 + s;
+        f1 = W::NR + (2 * p + 1) * KS2 + s;
+        src0 = li;
+        src1 = 16 + li;
+      }
+      const V g0 = transpose_frag<DT>(ja[i][0], ja[i][1], onehot_b<DT>(src0, lg));
+      const V g1 = transpose_frag<DT>(ja[i][0], ja[i][1], onehot_b<DT>(src1, lg));
+      *reinterpret_cast<V*>(frag_lds + f0 * 1024 + 16 * lane) = g0;
+      *reinterpret_cast<V*>(frag_lds + f1 * 1024 + 16 * lane) = g1;
+    }
+  }
+  lds_barrier();   // LDS only: the X loads stay in flight
+  if (t >= tokens) return;
+  V rf[NQ][2][KS1];
+  V lf[MB][KS2];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int ks = 0; ks < KS1; ++ks)
+        rf[q][h][ks] = *reinterpret_cast<const V*>(frag_lds + ((2 * q + h) * KS1 + ks) * 1024 + 16 * lane);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int s = 0; s < KS2; ++s)
+      lf[mb][s] = *reinterpret_cast<const V*>(frag_lds + (W::NR + mb * KS2 + s) * 1024 + 16 * lane);
+
+  while (true) {
+    // First product Z = X R, rounding point 1, accumulator -> A operand of the
+    // second product: zp[q][h][s][4e + r] = Z[16(2s + e) + 4lg + r][n(q, h, li)].
+    V zp[NQ][2][KS2];
+#pragma unroll
+    for (int s = 0; s < KS2; ++s) {
+      v4f acc[2][NQ][2];   // row blocks rb = 2s + e
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            acc[e][q][h] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS1; ++ks)
+              acc[e][q][h] = Ops::mfma(xf[2 * s + e][ks], rf[q][h][ks], acc[e][q][h]);
+          }
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const v4i w = {(int)Epi::pack(acc[0][q][h][0], acc[0][q][h][1]),
+                         (int)Epi::pack(acc[0][q][h][2], acc[0][q][h][3]),
+                         (int)Epi::pack(acc[1][q][h][0], acc[1][q][h][1]),
+                         (int)Epi::pack(acc[1][q][h][2], acc[1][q][h][3])};
+          zp[q][h][s] = __builtin_bit_cast(V, w);
+        }
+    }
+
+    // X is consumed: the next token's loads go into the same registers and
+    // arrive while this token's second product and epilogue run.
+    const int64_t tn = t + nwaves;
+    if (tn < tokens) fq_wave_load_x<DT, MB, NQ>(x + tn * x_ld, xf, li, lg);
+
+    // Second product, transposed (Y^T = Z^T L), rounding point 2. Lane (li, lg)
+    // of block (mb, q) holds Y[16mb + li][32q + 8lg + 4h + r]: packed word 4q + lg
+    // of row 16mb + li, nibbles r (h = 0) and r + 4 (h = 1).
+    uint32_t yp[MB][NQ][4];
+    uint32_t amax2 = 0u;   // max |Y| of the rounded values, as two 16-bit patterns
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS2; ++s) {
+          acc0 = Ops::mfma(zp[q][0][s], lf[mb][s], acc0);
+          acc1 = Ops::mfma(zp[q][1][s], lf[mb][s], acc1);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          yp[mb][q][r] = Epi::pack(acc0[r], acc1[r]);
+          amax2 = pk_absmax16(amax2, yp[mb][q][r]);
+        }
+      }
+    const uint32_t amax16 = wave_max_u32(max(amax2 & 0xFFFFu, amax2 >> 16));
+    const float s = fq_scale_abs<DT>(Epi::lo(amax16), clip);
+    if (lane == 0) out_scales[t] = s;
+
+    if (PACK && s > 0.f) {
+      const float rcp = 1.0f / s;
+      int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + lg;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          uint32_t word = 0u - Epi::kJunk;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) Epi::accumulate(word, yp[mb][q][r], rcp, r);
+          orow[(16 * mb + li) * (N / 8) + 4 * q] = (int32_t)word;
+        }
+    } else {
+      // int8 codes, and tokens whose scale rounded to 0 (the fallback's 0/0 codes)
+      const float rcp = 1.0f / s;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const int m = 16 * mb + li;
+          int code[8];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float y0 = Epi::lo(yp[mb][q][r]), y1 = Epi::hi(yp[mb][q][r]);
+            if (s > 0.f) {
+              code[r] = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y0 * rcp, -8.0f, 7.0f)));
+              code[4 + r] = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y1 * rcp, -8.0f, 7.0f)));
+            } else {
+              code[r] = fq_code_from_quot<PACK>(DT::round(opaque(y0) / s));
+              code[4 + r] = fq_code_from_quot<PACK>(DT::round(opaque(y1) / s));
+            }
+          }
+          if (PACK) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) word |= (uint32_t)(code[j] + 8) << (4 * j);
+            reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (N / 8) + 4 * q + lg] = (int32_t)word;
+          } else {
+            uint32_t lo4 = 0, hi4 = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              lo4 |= (uint32_t)(code[j] & 0xFF) << (8 * j);
+              hi4 |= (uint32_t)(code[4 + j] & 0xFF) << (8 * j);
+            }
+            v2i pair = {(int)lo4, (int)hi4};
+            *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + m * N + 32 * q + 8 * lg) = pair;
+          }
+        }
+    }
+
+    t = tn;
+    if (t >= tokens) break;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
 
@@ -563,11 +874,44 @@ static int launch_mfma(const void* x, int64_t tokens, int64_t x_ld, const void* 
   return QO_OK;
 }
 
+template <class DT, int MB, int NQ, bool PACK>
+static int launch_wave(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right,
+                       float clip, void* out_codes, float* out_scales, hipStream_t stream) {
+  using T = typename DT::T;
+  // one token per wave, up to two workgroups per CU; beyond that waves loop
+  const int64_t grid = std::min<int64_t>((tokens + kWaveKernelWaves - 1) / kWaveKernelWaves,
+                                         (int64_t)device_cu_count() * 2);
+  hipLaunchKernelGGL((fq_wave_kernel<DT, MB, NQ, PACK>), dim3((unsigned)grid), dim3(64 * kWaveKernelWaves), 0,
+                     stream,
+                     reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
+                     reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
+  return QO_OK;
+}
+
+// QO_FQ_NO_WAVE=1 keeps small shapes on fq_mfma_kernel (tests use it to
+// cross-check the two MFMA kernels).
+static bool fq_allow_wave() {
+  const char* e = getenv("QO_FQ_NO_WAVE");
+  return !(e && e[0] == '1');
+}
+
 template <class DT, bool PACK>
 static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_ld, const void* left,
                          const void* right, float clip, void* out_codes, float* out_scales,
                          hipStream_t stream, bool* handled) {
   *handled = true;
+  // the wave kernel takes the scale from max |Y|, which needs clip > 0
+  if (fq_allow_wave() && clip > 0.f && clip <= 3.4e38f) {
+#define QO_FQ_WAVE_CASE(MB_, NQ_)                                                                    \
+    if (M == 16 * (MB_) && N == 32 * (NQ_))                                                          \
+      return launch_wave<DT, MB_, NQ_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, \
+                                             stream);
+    QO_FQ_WAVE_CASE(4, 2)   // 64 x 64 (hidden 4096)
+    QO_FQ_WAVE_CASE(2, 2)   // 32 x 64 (hidden 2048)
+    QO_FQ_WAVE_CASE(2, 1)   // 32 x 32 (hidden 1024)
+    QO_FQ_WAVE_CASE(4, 1)   // 64 x 32 (hidden 2048)
+#undef QO_FQ_WAVE_CASE
+  }
 #define QO_FQ_CASE(MB_, NP_)                                                                      \
   if (M == 16 * (MB_) && N == 32 * (NP_))                                                         \
     return launch_mfma<DT, MB_, NP_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, \
@@ -612,7 +956,9 @@ static int run_quantize(const void* x, int64_t tokens, int64_t x_ld, const void*
                         int N, float clip, void* out_codes, float* out_scales, hipStream_t stream,
                         bool allow_mfma) {
   if constexpr (DT::code != QO_DTYPE_F32) {
-    const bool aligned = ((uintptr_t)x % 16 == 0) && ((x_ld * (int64_t)sizeof(typename DT::T)) % 16 == 0);
+    // 16-byte vector loads of X rows and of L / R rows
+    const bool aligned = ((uintptr_t)x % 16 == 0) && ((x_ld * (int64_t)sizeof(typename DT::T)) % 16 == 0) &&
+                         ((uintptr_t)left % 16 == 0) && ((uintptr_t)right % 16 == 0);
     if (allow_mfma && aligned) {
       bool handled = false;
       int st = dispatch_mfma<DT, PACK>(M, N, x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream,

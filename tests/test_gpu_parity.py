@@ -108,6 +108,8 @@ SHAPES = [
     (7, 48, 64, torch.bfloat16, 1.0, True),
     (6, 96, 128, torch.float16, 0.8, False),
     (4, 32, 32, torch.float16, 1.0, True),
+    (7, 64, 32, torch.bfloat16, 0.9, True),
+    (5000, 64, 64, torch.float16, 0.9, True),    # more tokens than resident waves: waves loop
     (11, 16, 16, torch.bfloat16, 1.0, True),     # generic kernel (N not a multiple of 32)
     (2, 8, 8, torch.float16, 0.9, False),        # generic kernel
     (5, 12, 20, torch.float32, 1.0, False),      # generic kernel, fp32
@@ -137,6 +139,25 @@ def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
     d = (_codes_int8(q1, True).int() - _codes_int8(q2, True).int()).abs()
     assert int(d.max()) <= 1 and float((d != 0).float().mean()) <= CODE_FLIP_FRAC
     assert float(((s1 - s2).abs() / s2.abs()).max()) <= SCALE_RTOL
+
+
+@pytest.mark.parametrize("pack", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mn", [(64, 64), (32, 64), (32, 32)])
+@pytest.mark.parametrize("tokens", [1, 203, 4099])
+def test_quantize_wave_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack, monkeypatch):
+    """The wave-per-token kernel and the workgroup kernel use the same fragment
+    layouts and k order, so their codes and scales agree bit for bit."""
+    m, n = mn
+    case = wl.quant_case("wave", tokens, m, n, dtype, 0.9, pack, seed=tokens + m + n, outlier_frac=0.01,
+                         outlier_scale=20.0)
+    case.x[tokens // 2].zero_()
+    _say(f"wave vs group kernel T={tokens} {m}x{n} {dtype} pack={pack}")
+    q1, s1 = run_capi_quant(case, gpu)
+    monkeypatch.setenv("QO_FQ_NO_WAVE", "1")
+    q2, s2 = run_capi_quant(case, gpu)
+    monkeypatch.delenv("QO_FQ_NO_WAVE")
+    assert torch.equal(s1, s2) and torch.equal(q1, q2)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
