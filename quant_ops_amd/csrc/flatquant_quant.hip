@@ -558,8 +558,9 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 //   into that order: D[4lg + r][li] = A[4lg + r][sel(li)], exact, since every
 //   output is one product with 1.0 plus zeros. The waves split the build,
 //   exchange the fragments through LDS (one barrier) and keep them in VGPRs.
-// * The column permutation and the transposed second product are those of
-//   fq_mfma_kernel, so each lane ends with the 8 features of one packed word.
+// * The second product runs transposed as in fq_mfma_kernel, and a column
+//   permutation (wave_col) leaves each lane with whole packed words, adjacent
+//   ones, so every store instruction writes 16 complete rows of codes.
 // * The scale needs only an in-wave reduction.
 //
 // Waves loop over tokens (stride = all waves of the grid); the next token's X
@@ -594,14 +595,17 @@ __device__ inline typename MfmaOps<DT>::V onehot_b(int src, int lg) {
 // Two selection products of the rows tiles a0 (slots j = 0..3) and a1 (slots
 // j = 4..7) assembled into one 8-element fragment (values are exact in D).
 template <class DT>
-__device__ inline typename MfmaOps<DT>::V transpose_frag(typename MfmaOps<DT>::V a0, typename MfmaOps<DT>::V a1,
-                                                        typename MfmaOps<DT>::V sel) {
-  const v4f z = {0.f, 0.f, 0.f, 0.f};
-  const v4f d0 = MfmaOps<DT>::mfma(a0, sel, z);
-  const v4f d1 = MfmaOps<DT>::mfma(a1, sel, z);
+__device__ inline typename MfmaOps<DT>::V pack_frag(v4f d0, v4f d1) {
   const v4i w = {(int)FqEpi<DT>::pack(d0[0], d0[1]), (int)FqEpi<DT>::pack(d0[2], d0[3]),
                  (int)FqEpi<DT>::pack(d1[0], d1[1]), (int)FqEpi<DT>::pack(d1[2], d1[3])};
   return __builtin_bit_cast(typename MfmaOps<DT>::V, w);
+}
+
+template <class DT>
+__device__ inline typename MfmaOps<DT>::V transpose_frag(typename MfmaOps<DT>::V a0, typename MfmaOps<DT>::V a1,
+                                                        typename MfmaOps<DT>::V sel) {
+  const v4f z = {0.f, 0.f, 0.f, 0.f};
+  return pack_frag<DT>(MfmaOps<DT>::mfma(a0, sel, z), MfmaOps<DT>::mfma(a1, sel, z));
 }
 
 template <class DT, int MB, int NQ>
@@ -620,6 +624,19 @@ __device__ inline void fq_wave_load_x(const typename DT::T* __restrict__ xt,
 // per lane). A build job is one pair of row tiles and the two fragments its
 // selection products give: R job (q, ks) -> rf[q][0..1][ks], L job (s, p) ->
 // lf[2p..2p+1][s].
+// Store N adjacent 32-bit words (N = 1, 2 or 4) with one instruction.
+template <int NW_>
+__device__ inline void store_words(int32_t* dst, const uint32_t (&w)[NW_]) {
+  if constexpr (NW_ == 1) {
+    *dst = (int32_t)w[0];
+  } else if constexpr (NW_ == 2) {
+    *reinterpret_cast<v2i*>(dst) = v2i{(int)w[0], (int)w[1]};
+  } else {
+    static_assert(NW_ == 4, "1, 2 or 4 words");
+    *reinterpret_cast<v4i*>(dst) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  }
+}
+
 template <int MB, int NQ>
 struct WaveFrags {
   static constexpr int KS1 = NQ, KS2 = MB / 2;
@@ -630,6 +647,17 @@ struct WaveFrags {
 };
 
 constexpr int kWaveKernelWaves = 8;
+
+// Column permutation of the wave kernel: MFMA block (q, h) of the first
+// product, lane column i, is physical column n = 8 NQ (i/4) + 8q + 4h + i%4.
+// After the transposed second product, lane (li, lg) of block (q, h) holds the
+// columns 8 (NQ lg + q) + 4h + r: packed word NQ lg + q, nibbles 4h + r. The
+// lane's NQ words of a row are adjacent, so one store per row block writes 16
+// whole rows.
+template <int NQ>
+__device__ inline int wave_col(int q, int h, int i) {
+  return 8 * NQ * (i >> 2) + 8 * q + 4 * h + (i & 3);
+}
 
 template <class DT, int MB, int NQ, bool PACK>
 __global__ void __launch_bounds__(64 * kWaveKernelWaves)
@@ -646,73 +674,74 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   constexpr int M = 16 * MB, N = 32 * NQ, F = M * N;
   constexpr int KS1 = W::KS1;    // 32-deep slabs of the first product (k = n')
   constexpr int KS2 = W::KS2;    // 32-deep slabs of the second product (k = m')
-  constexpr int JPW = (W::NJ + NW - 1) / NW;
+  static_assert(W::NJ <= NW, "one fragment build job per wave at most");
   __shared__ __align__(16) unsigned char frag_lds[W::NF * 1024];
 
   const int lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t nwaves = (int64_t)gridDim.x * NW;
   int64_t t = (int64_t)blockIdx.x * NW + wave;
 
-  // Row tiles of this wave's build jobs first, then the first token's X: the
-  // fragment build below waits only for the tiles (loads retire in order)
-  // while X is still in flight. No branches around these loads (a branch
-  // would make the compiler's wait counts conservative): a wave without a job
-  // repeats the last one and writes the same bytes to the same place, a wave
-  // without a token loads the last token and stores nothing.
-  //   R job (q, ks): A_e[i][k] = R[32ks + 8(i/4) + i%4 + 4e][32q + k]
-  //   L job (s, p):  A_e[i][k] = L[32s + 16e + i][32p + k]
-  V ja[JPW][2];
+  // Row tiles of this wave's build job first, then the first token's X: the
+  // build below waits only for the tiles (loads retire in order) while X is
+  // still in flight. No divergent branch precedes the X loads, so the
+  // compiler's wait counts stay exact: a wave without a job repeats the last
+  // one (same bytes to the same place), a wave without a token loads the last
+  // token and stores nothing.
+  //   R job (q, ks), tile (c, e): A[i][k] = R[32ks + 8(i/4) + i%4 + 4e][32c + k]
+  //   L job (s, p),  tile (0, e): A[i][k] = L[32s + 16e + i][32p + k]
+  const int j = min(wave, W::NJ - 1);
+  const bool rjob = j < W::JR;
+  V ra[NQ][2], la[2];
+  if (rjob) {
+    const int ks = j % KS1;
 #pragma unroll
-  for (int i = 0; i < JPW; ++i) {
-    const int j = min(wave + i * NW, W::NJ - 1);
-    {
-      const T* base;
-      int off1;
-      if (j < W::JR) {
-        const int q = j / KS1, ks = j % KS1;
-        base = right + (32 * ks + 8 * (li >> 2) + (li & 3)) * N + 32 * q + 8 * lg;
-        off1 = 4 * N;
-      } else {
-        const int s = (j - W::JR) / (MB / 2), p = (j - W::JR) % (MB / 2);
-        base = left + (32 * s + li) * M + 32 * p + 8 * lg;
-        off1 = 16 * M;
-      }
-      ja[i][0] = *reinterpret_cast<const V*>(base);
-      ja[i][1] = *reinterpret_cast<const V*>(base + off1);
+    for (int c = 0; c < NQ; ++c) {
+      const T* base = right + (32 * ks + 8 * (li >> 2) + (li & 3)) * N + 32 * c + 8 * lg;
+      ra[c][0] = *reinterpret_cast<const V*>(base);
+      ra[c][1] = *reinterpret_cast<const V*>(base + 4 * N);
     }
+  } else {
+    const int s = (j - W::JR) / (MB / 2), p = (j - W::JR) % (MB / 2);
+    const T* base = left + (32 * s + li) * M + 32 * p + 8 * lg;
+    la[0] = *reinterpret_cast<const V*>(base);
+    la[1] = *reinterpret_cast<const V*>(base + 16 * M);
   }
   V xf[MB][KS1];
   fq_wave_load_x<DT, MB, NQ>(x + min(t, tokens - 1) * x_ld, xf, li, lg);
 
-  // Build: selection sel_h(li) = 8(li/4) + 4h + li%4 gives R's permuted pair
-  // columns, sel_c(li) = 16c + li the two 16-column halves of an L tile:
-  //   rf[q][h][ks][j] = R[32ks + 8lg + j][32q + 8(li/4) + 4h + li%4]
-  //   lf[mb][s][j]    = L[32s + 16(j/4) + 4lg + j%4][16mb + li]
+  // Build (selection products, exact):
+  //   rf[q][h][ks][j] = R[32ks + 8lg + j][wave_col(q, h, li)], summed over the
+  //                     column tiles c (only the tile holding the column selects)
+  //   lf[mb][s][j]    = L[32s + 16(j/4) + 4lg + j%4][16mb + li], mb = 2p + cc
+  {
+    int f0, f1;
+    V g0, g1;
+    if (rjob) {
+      const int q = j / KS1, ks = j % KS1;
+      f0 = (2 * q) * KS1 + ks;
+      f1 = (2 * q + 1) * KS1 + ks;
+      v4f d[2][2] = {};
 #pragma unroll
-  for (int i = 0; i < JPW; ++i) {
-    const int j = min(wave + i * NW, W::NJ - 1);
-    {
-      int f0, f1, src0, src1;
-      if (j < W::JR) {
-        const int q = j / KS1, ks = j % KS1;
-        f0 = (2 * q) * KS1 + ks;
-        f1 = (2 * q + 1) * KS1 + ks;
-        src0 = 8 * (li >> 2) + (li & 3);
-        src1 = src0 + 4;
-      } else {
-        const int s = (j - W::JR) / (MB / 2), p = (j - W::JR) % (MB / 2);
-        f0 = W::NR + (2 * p) * KS2 + s;
-        f1 = W::NR + (2 * p + 1) * KS2 + s;
-        src0 = li;
-        src1 = 16 + li;
-      }
-      const V g0 = transpose_frag<DT>(ja[i][0], ja[i][1], onehot_b<DT>(src0, lg));
-      const V g1 = transpose_frag<DT>(ja[i][0], ja[i][1], onehot_b<DT>(src1, lg));
-      *reinterpret_cast<V*>(frag_lds + f0 * 1024 + 16 * lane) = g0;
-      *reinterpret_cast<V*>(frag_lds + f1 * 1024 + 16 * lane) = g1;
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int c = 0; c < NQ; ++c) {
+          const V sel = onehot_b<DT>(wave_col<NQ>(q, h, li) - 32 * c, lg);
+          d[h][0] = Ops::mfma(ra[c][0], sel, d[h][0]);
+          d[h][1] = Ops::mfma(ra[c][1], sel, d[h][1]);
+        }
+      g0 = pack_frag<DT>(d[0][0], d[0][1]);
+      g1 = pack_frag<DT>(d[1][0], d[1][1]);
+    } else {
+      const int s = (j - W::JR) / (MB / 2), p = (j - W::JR) % (MB / 2);
+      f0 = W::NR + (2 * p) * KS2 + s;
+      f1 = W::NR + (2 * p + 1) * KS2 + s;
+      g0 = transpose_frag<DT>(la[0], la[1], onehot_b<DT>(li, lg));
+      g1 = transpose_frag<DT>(la[0], la[1], onehot_b<DT>(16 + li, lg));
     }
+    *reinterpret_cast<V*>(frag_lds + f0 * 1024 + 16 * lane) = g0;
+    *reinterpret_cast<V*>(frag_lds + f1 * 1024 + 16 * lane) = g1;
   }
   lds_barrier();   // LDS only: the X loads stay in flight
   if (t >= tokens) return;
@@ -733,7 +762,7 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 
   while (true) {
     // First product Z = X R, rounding point 1, accumulator -> A operand of the
-    // second product: zp[q][h][s][4e + r] = Z[16(2s + e) + 4lg + r][n(q, h, li)].
+    // second product: zp[q][h][s][4e + r] = Z[16(2s + e) + 4lg + r][wave_col(q, h, li)].
     V zp[NQ][2][KS2];
 #pragma unroll
     for (int s = 0; s < KS2; ++s) {
@@ -767,8 +796,8 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
     if (tn < tokens) fq_wave_load_x<DT, MB, NQ>(x + tn * x_ld, xf, li, lg);
 
     // Second product, transposed (Y^T = Z^T L), rounding point 2. Lane (li, lg)
-    // of block (mb, q) holds Y[16mb + li][32q + 8lg + 4h + r]: packed word 4q + lg
-    // of row 16mb + li, nibbles r (h = 0) and r + 4 (h = 1).
+    // of block (mb, q) holds Y[16mb + li][8(NQ lg + q) + 4h + r]: packed word
+    // NQ lg + q of row 16mb + li, nibbles r (h = 0) and r + 4 (h = 1).
     uint32_t yp[MB][NQ][4];
     uint32_t amax2 = 0u;   // max |Y| of the rounded values, as two 16-bit patterns
 #pragma unroll
@@ -793,16 +822,18 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 
     if (PACK && s > 0.f) {
       const float rcp = 1.0f / s;
-      int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + lg;
+      int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + NQ * lg;
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
+      for (int mb = 0; mb < MB; ++mb) {
+        uint32_t words[NQ];
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-          uint32_t word = 0u - Epi::kJunk;
+          words[q] = 0u - Epi::kJunk;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) Epi::accumulate(word, yp[mb][q][r], rcp, r);
-          orow[(16 * mb + li) * (N / 8) + 4 * q] = (int32_t)word;
+          for (int r = 0; r < 4; ++r) Epi::accumulate(words[q], yp[mb][q][r], rcp, r);
         }
+        store_words<NQ>(orow + (16 * mb + li) * (N / 8), words);
+      }
     } else {
       // int8 codes, and tokens whose scale rounded to 0 (the fallback's 0/0 codes)
       const float rcp = 1.0f / s;
@@ -827,7 +858,7 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
             uint32_t word = 0;
 #pragma unroll
             for (int j = 0; j < 8; ++j) word |= (uint32_t)(code[j] + 8) << (4 * j);
-            reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (N / 8) + 4 * q + lg] = (int32_t)word;
+            reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (N / 8) + NQ * lg + q] = (int32_t)word;
           } else {
             uint32_t lo4 = 0, hi4 = 0;
 #pragma unroll
@@ -836,7 +867,8 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
               hi4 |= (uint32_t)(code[4 + j] & 0xFF) << (8 * j);
             }
             v2i pair = {(int)lo4, (int)hi4};
-            *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + m * N + 32 * q + 8 * lg) = pair;
+            *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + m * N + 8 * (NQ * lg + q)) =
+                pair;
           }
         }
     }
