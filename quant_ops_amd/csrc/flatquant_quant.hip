@@ -228,6 +228,44 @@ struct FqEpi<F16T> {
   }
   static constexpr uint32_t kJunk =
       0x66006600u + (0x66006600u << 4) + (0x66006600u << 8) + (0x66006600u << 12);
+
+  // Packed word of four pairs (nibbles r and r + 4 from pair r), clamping the
+  // rounded pair instead of the float32 quotients: rounding is monotonic and
+  // -8, 7 are fp16 values, so clamp(rnd(a)) = rnd(clamp(a)). One packed min per
+  // pair, plus one packed max when a quotient can round below -8.5 (LOW).
+  template <bool LOW>
+  __device__ static inline uint32_t word4(const uint32_t (&p)[4], float rcp) {
+    const v2h seven = {(_Float16)7.0f, (_Float16)7.0f};
+    const v2h minus8 = {(_Float16)-8.0f, (_Float16)-8.0f};
+    const v2h magic = {(_Float16)1544.0f, (_Float16)1544.0f};
+    uint32_t word = 0u - kJunk;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      v2h t = __builtin_bit_cast(v2h, pack(mul_f16lo(p[r], rcp), mul_f16hi(p[r], rcp)));
+      t = __builtin_elementwise_min(t, seven);
+      if (LOW) t = __builtin_elementwise_max(t, minus8);
+      t = t + magic;
+      word += __builtin_bit_cast(uint32_t, t) << (4 * r);
+    }
+    return word;
+  }
+
+  // Running extremes of rounded Y pairs, two pairs per step (v_pk_maximum3 /
+  // v_pk_minimum3), and max |y| from them as a 16-bit pattern.
+  struct Amax {
+    v2h hi = {(_Float16)-INFINITY, (_Float16)-INFINITY};
+    v2h lo = {(_Float16)INFINITY, (_Float16)INFINITY};
+  };
+  __device__ static inline void track2(Amax& a, uint32_t p0, uint32_t p1) {
+    const v2h y0 = __builtin_bit_cast(v2h, p0), y1 = __builtin_bit_cast(v2h, p1);
+    a.hi = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a.hi, y0), y1);
+    a.lo = __builtin_elementwise_minimum(__builtin_elementwise_minimum(a.lo, y0), y1);
+  }
+  __device__ static inline uint32_t amax_bits(const Amax& a) {
+    const uint32_t m = pk_absmax16(pk_absmax16(0u, __builtin_bit_cast(uint32_t, a.hi)),
+                                   __builtin_bit_cast(uint32_t, a.lo));
+    return max(m & 0xFFFFu, m >> 16);
+  }
 };
 
 template <>
@@ -252,6 +290,25 @@ struct FqEpi<BF16T> {
   }
   static constexpr uint32_t kJunk =
       0x4B400000u + (0x4B400000u << 4) + (0x4B400000u << 8) + (0x4B400000u << 12);
+
+  // Packed word of four pairs (the float32 clamp covers both bounds).
+  template <bool LOW>
+  __device__ static inline uint32_t word4(const uint32_t (&p)[4], float rcp) {
+    uint32_t word = 0u - kJunk;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) accumulate(word, p[r], rcp, r);
+    return word;
+  }
+
+  // max |y| of rounded Y pairs as a 16-bit pattern (sign-cleared bf16 bits
+  // order like the values).
+  struct Amax {
+    uint32_t m = 0u;
+  };
+  __device__ static inline void track2(Amax& a, uint32_t p0, uint32_t p1) {
+    a.m = pk_absmax16(pk_absmax16(a.m, p0), p1);
+  }
+  __device__ static inline uint32_t amax_bits(const Amax& a) { return max(a.m & 0xFFFFu, a.m >> 16); }
 };
 
 template <int MB, int NP>
@@ -637,6 +694,19 @@ __device__ inline void store_words(int32_t* dst, const uint32_t (&w)[NW_]) {
   }
 }
 
+// Packed codes of a wave kernel token: lane (li, lg) writes row 16mb + li,
+// words NQ lg .. NQ lg + NQ - 1 (orow already offset by NQ lg).
+template <class DT, int MB, int NQ, bool LOW>
+__device__ inline void fq_wave_store_codes(int32_t* orow, const uint32_t (&yp)[MB][NQ][4], float rcp, int li) {
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    uint32_t words[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) words[q] = FqEpi<DT>::template word4<LOW>(yp[mb][q], rcp);
+    store_words<NQ>(orow + (16 * mb + li) * (4 * NQ), words);
+  }
+}
+
 template <int MB, int NQ>
 struct WaveFrags {
   static constexpr int KS1 = NQ, KS2 = MB / 2;
@@ -799,7 +869,7 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
     // of block (mb, q) holds Y[16mb + li][8(NQ lg + q) + 4h + r]: packed word
     // NQ lg + q of row 16mb + li, nibbles r (h = 0) and r + 4 (h = 1).
     uint32_t yp[MB][NQ][4];
-    uint32_t amax2 = 0u;   // max |Y| of the rounded values, as two 16-bit patterns
+    typename Epi::Amax am;
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
@@ -811,29 +881,23 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
           acc1 = Ops::mfma(zp[q][1][s], lf[mb][s], acc1);
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          yp[mb][q][r] = Epi::pack(acc0[r], acc1[r]);
-          amax2 = pk_absmax16(amax2, yp[mb][q][r]);
-        }
+        for (int r = 0; r < 4; ++r) yp[mb][q][r] = Epi::pack(acc0[r], acc1[r]);
+        Epi::track2(am, yp[mb][q][0], yp[mb][q][1]);
+        Epi::track2(am, yp[mb][q][2], yp[mb][q][3]);
       }
-    const uint32_t amax16 = wave_max_u32(max(amax2 & 0xFFFFu, amax2 >> 16));
-    const float s = fq_scale_abs<DT>(Epi::lo(amax16), clip);
+    const float amax = Epi::lo(wave_max_u32(Epi::amax_bits(am)));
+    const float s = fq_scale_abs<DT>(amax, clip);
     if (lane == 0) out_scales[t] = s;
 
     if (PACK && s > 0.f) {
       const float rcp = 1.0f / s;
       int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + NQ * lg;
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        uint32_t words[NQ];
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-          words[q] = 0u - Epi::kJunk;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) Epi::accumulate(words[q], yp[mb][q][r], rcp, r);
-        }
-        store_words<NQ>(orow + (16 * mb + li) * (N / 8), words);
-      }
+      // Quotients are >= -rnd(amax * rcp); below -8.5 they would need the
+      // lower clamp (rne(-8.5) = -8). Uniform per token.
+      if (DT::round(amax * rcp) > 8.5f)
+        fq_wave_store_codes<DT, MB, NQ, true>(orow, yp, rcp, li);
+      else
+        fq_wave_store_codes<DT, MB, NQ, false>(orow, yp, rcp, li);
     } else {
       // int8 codes, and tokens whose scale rounded to 0 (the fallback's 0/0 codes)
       const float rcp = 1.0f / s;
