@@ -19,6 +19,7 @@
 // Generic kernel (gemm_i4_generic): one output per thread, any strides and
 // sizes (K < 2^21). Used when the fast kernel's layout / alignment
 // requirements are not met.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -333,6 +334,12 @@ __device__ inline void dma16(const void* src, uint32_t lds) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
 }
 
+// The same copy addressed as a wave-uniform 64-bit base (SGPRs) plus the
+// lane's 32-bit byte offset.
+__device__ inline void dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+
 template <int N>
 __device__ inline void gemm_wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt out of range");
@@ -561,6 +568,209 @@ gemm_i4_dma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restric
 }
 
 // ---------------------------------------------------------------------------
+// Register-prefetch variant of gemm_i4_dma (gemm_i4_pp): the same LDS-DMA ring
+// and operand layout, but a stage's packed words are read from LDS into a
+// second register set while the previous stage's MFMAs run, so LDS latency is
+// never waited on between MFMAs. Step s (buffer J = s % STAGES, registers
+// P = s % 2, filled during step s - 1):
+//   wait for this wave's DMA of stage s + 1; lgkmcnt(0) + barrier (every
+//   wave's share of stage s + 1 has landed and every wave holds stage s in
+//   registers, so buffer J is free); DMA stage s + STAGES into buffer J; read
+//   stage s + 1 into registers 1 - P; widen and multiply stage s.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool B_NK, class OT>
+__global__ void __launch_bounds__(64 * WGM * WGN, 1)
+gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
+           const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
+           typename OT::T* __restrict__ out, int64_t ldc, int M, int N, int K, int tiles_m) {
+  using S = DmaStage<BM, BN, B_NK>;
+  constexpr int W = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int FM = WM / 16, FN = WN / 16;
+  constexpr int PER = (S::DMA + W - 1) / W;   // DMA instructions per wave per stage
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile");
+  static_assert(STAGES >= 2 && STAGES <= 4 && STAGES % 2 == 0, "stages (even: register sets alternate)");
+  static_assert(PER * (STAGES - 1) < 64, "vmcnt range");
+
+  __shared__ __align__(16) unsigned char st0[S::BYTES];
+  __shared__ __align__(16) unsigned char st1[S::BYTES];
+  __shared__ __align__(16) unsigned char st2[STAGES > 2 ? S::BYTES : 16];
+  __shared__ __align__(16) unsigned char st3[STAGES > 3 ? S::BYTES : 16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int li = lane & 15, lg = lane >> 4;
+
+  const int nblk = gridDim.x;
+  int pid = blockIdx.x;
+  if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
+  const int tm = pid % tiles_m, tn = pid / tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = K >> 7;
+
+  // Copy t of this wave reads base + voff[t] (+ the stage's advance): the
+  // base is wave-uniform (SGPRs), voff the lane's 32-bit byte offset inside
+  // the tile. Rows and columns past the matrix edge are clamped; they only
+  // feed accumulators that are never stored. Spare slots repeat the last copy.
+  const char* const a_base = reinterpret_cast<const char*>(a + (int64_t)m0 * lda);
+  const char* const b_base = reinterpret_cast<const char*>(B_NK ? b + (int64_t)n0 * ldb : b + n0);
+  const int64_t b_adv = B_NK ? 64 : 64 * ldb;   // bytes per stage
+  bool is_a[PER];
+  uint32_t dst[PER], voff[PER];
+#pragma unroll
+  for (int t = 0; t < PER; ++t) {
+    int i = __builtin_amdgcn_readfirstlane(wave) + W * t;
+    i = i < S::DMA ? i : S::DMA - 1;
+    is_a[t] = i < S::A_DMA;
+    if (i < S::A_DMA) {
+      voff[t] = (uint32_t)(min(16 * i + li, M - 1 - m0) * (int)lda * 4 + 16 * lg);
+      dst[t] = i * 1024;
+    } else if (B_NK) {
+      const int c = i - S::A_DMA;
+      voff[t] = (uint32_t)(min(16 * c + li, N - 1 - n0) * (int)ldb * 4 + 16 * lg);
+      dst[t] = S::A_BYTES + c * 1024;
+    } else {
+      const int p = i - S::A_DMA;
+      voff[t] = (uint32_t)(p * (int)ldb * 4 + 4 * min(4 * lane, N - 4 - n0));
+      dst[t] = S::A_BYTES + p * S::KN_ROW;
+    }
+  }
+
+  auto stage_ptr = [&](auto buf) -> unsigned char* {
+    constexpr int J = decltype(buf)::value;
+    if constexpr (J == 0) return st0;
+    else if constexpr (J == 1) return st1;
+    else if constexpr (J == 2) return st2;
+    else return st3;
+  };
+  auto issue = [&](int ks, auto buf) {
+    const uint32_t base =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)stage_ptr(buf);
+    const char* ab = a_base + 64 * (int64_t)ks;
+    const char* bb = b_base + b_adv * ks;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) dma16_s(voff[t], is_a[t] ? ab : bb, base + dst[t]);
+  };
+
+  v4i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  v4i ar[2][FM], br[2][FN];
+  auto load_regs = [&](auto buf, auto set) {
+    constexpr int P = decltype(set)::value;
+    const unsigned char* base = stage_ptr(buf);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      ar[P][i] = *reinterpret_cast<const v4i*>(base + (wm * FM + i) * 1024 + 16 * lane);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (B_NK) {
+        br[P][j] = *reinterpret_cast<const v4i*>(base + S::A_BYTES + (wn * FN + j) * 1024 + 16 * lane);
+      } else {
+        const unsigned char* col = base + S::A_BYTES + (wn * WN + 16 * j + li) * 4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) br[P][j][t] = *reinterpret_cast<const int*>(col + (4 * lg + t) * S::KN_ROW);
+      }
+    }
+  };
+  auto compute = [&](auto set) {
+    constexpr int P = decltype(set)::value;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4i fa[FM];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) fa[i] = widen_pair(ar[P][i][2 * h], ar[P][i][2 * h + 1]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const v4i fb = widen_pair(br[P][j][2 * h], br[P][j][2 * h + 1]);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, fa[i], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+  auto step_stage = [&](int s, auto buf, auto set) {
+    constexpr int J = decltype(buf)::value;
+    constexpr int P = decltype(set)::value;
+    gemm_wait_vmcnt<PER * (STAGES - 2)>();
+    // lgkmcnt(0) and the barrier as builtins: the compiler's wait tracking then
+    // knows this stage's registers have arrived and adds no wait of its own
+    // after the next stage's reads are issued. The builtins do not order
+    // memory accesses, so empty asm statements with a memory clobber keep the
+    // previous step's LDS reads above them and this step's below.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt / expcnt unchanged (max)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(min(s + STAGES, nk - 1), buf);
+    load_regs(std::integral_constant<int, (J + 1) % STAGES>{}, std::integral_constant<int, 1 - P>{});
+    compute(set);
+  };
+
+  issue(0, std::integral_constant<int, 0>{});
+  issue(min(1, nk - 1), std::integral_constant<int, 1>{});
+  if constexpr (STAGES > 2) issue(min(2, nk - 1), std::integral_constant<int, 2>{});
+  if constexpr (STAGES > 3) issue(min(3, nk - 1), std::integral_constant<int, 3>{});
+  gemm_wait_vmcnt<PER * (STAGES - 1)>();
+  asm volatile("s_barrier" ::: "memory");
+  load_regs(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+  for (int s = 0; s < nk; s += STAGES) {
+    step_stage(s, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    if (s + 1 < nk) step_stage(s + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    if constexpr (STAGES > 2)
+      if (s + 2 < nk) step_stage(s + 2, std::integral_constant<int, 2>{}, std::integral_constant<int, 0>{});
+    if constexpr (STAGES > 3)
+      if (s + 3 < nk) step_stage(s + 3, std::integral_constant<int, 3>{}, std::integral_constant<int, 1>{});
+  }
+  gemm_wait_vmcnt<0>();
+
+  using T = typename OT::T;
+  float sav[FM], sbv[FN][4];
+  with_scale_dtype(sad, [&](auto dt) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) sav[i] = scale_at<decltype(dt)::value>(sa, min(m0 + wm * WM + 16 * i + li, M - 1));
+  });
+  with_scale_dtype(sbd, [&](auto dt) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sbv[j][r] = scale_at<decltype(dt)::value>(sb, min(n0 + wn * WN + 16 * j + 4 * lg + r, N - 1));
+  });
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * WM + 16 * i + li;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WN + 16 * j + 4 * lg;
+      if (n >= N) continue;
+      T v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(acc[i][j][r] >> 8, sav[i], sbv[j][r]));
+      T* o = out + (int64_t)m * ldc + n;
+      if (n + 3 < N) {
+        if constexpr (sizeof(T) == 2) {
+          typedef short v4s __attribute__((ext_vector_type(4)));
+          v4s pk;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
+          *reinterpret_cast<v4s*>(o) = pk;
+        } else {
+          *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) o[r] = v[r];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host dispatch.
 // ---------------------------------------------------------------------------
 
@@ -590,21 +800,20 @@ static void launch_mfma(const int32_t* a, int64_t lda, const int32_t* b, int64_t
                      tiles_n);
 }
 
-#ifndef QO_GEMM_DMA_WAVES
-#define QO_GEMM_DMA_WAVES 4, 2
-#endif
-#ifndef QO_GEMM_DMA_STAGES
-#define QO_GEMM_DMA_STAGES 4
-#endif
-
+// Launch of the pipelined kernels: 4 x 2 waves, four-stage ring. The W.t()
+// layout (B_NK) takes the register-prefetch kernel gemm_i4_pp; the row-major
+// [K/8, N] layout keeps gemm_i4_dma, whose four 4-byte column reads per
+// operand would not fit a second register set within 256 VGPRs.
 template <int BM, int BN, bool B_NK, class OT>
 static void launch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
                        const void* sb, int sbd, void* out, int64_t ldc, int M, int N, int K, hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  constexpr int WGM_WGN[2] = {QO_GEMM_DMA_WAVES};
-  hipLaunchKernelGGL((gemm_i4_dma<BM, BN, WGM_WGN[0], WGM_WGN[1], QO_GEMM_DMA_STAGES, B_NK, OT>),
-                     dim3(tiles_m * tiles_n), dim3(64 * WGM_WGN[0] * WGM_WGN[1]), 0, stream, a, lda, b, ldb, sa,
-                     sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, M, N, K, tiles_m);
+  if constexpr (B_NK)
+    hipLaunchKernelGGL((gemm_i4_pp<BM, BN, 4, 2, 4, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a,
+                       lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, M, N, K, tiles_m);
+  else
+    hipLaunchKernelGGL((gemm_i4_dma<BM, BN, 4, 2, 4, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a,
+                       lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, M, N, K, tiles_m);
 }
 
 // Fraction of the machine's workgroup slots doing useful output in a launch
@@ -615,6 +824,7 @@ static double tile_efficiency(int64_t M, int64_t N, int BM, int BN, int cus) {
   const int64_t tiles = tm * tn, rounds = (tiles + cus - 1) / cus;
   return (double)(M * N) / ((double)rounds * cus * BM * BN);
 }
+
 
 static int gemm_cu_count() {
   static int cached = 0;
@@ -646,7 +856,9 @@ static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bs
   const bool b_nk = (bsp == 1);
   const bool b_kn = (bsn == 1) && !b_nk;
   const int64_t ldb = b_nk ? bsn : bsp;
-  const bool fits = M <= INT32_MAX / 2 && N <= INT32_MAX / 2 && K <= 65536;
+  // 32-bit in-tile byte offsets of the pipelined kernels: 256 rows of A or B
+  const bool fits = M <= INT32_MAX / 2 && N <= INT32_MAX / 2 && K <= 65536 && lda < (1 << 21) &&
+                    ldb < (1 << 21);
   const bool aligned = ((uintptr_t)a % 16 == 0) && (lda % 4 == 0) && ((uintptr_t)b % 16 == 0) && (ldb % 4 == 0) &&
                        ((uintptr_t)out % (4 * sizeof(T)) == 0) && (ldc % 4 == 0);
   if (allow_fast && fits && aligned && (b_nk || b_kn)) {
