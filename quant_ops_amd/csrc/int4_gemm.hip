@@ -771,6 +771,127 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// Skinny kernel (gemm_i4_skinny): M <= 64, the decode shapes. The time is the
+// read of B, so the work is spread over columns and K instead of tiles: a
+// workgroup owns 16 output columns and all M rows; its 8 waves split K into
+// contiguous slices of 128-deep stages, stream their slice of B and A from
+// global memory straight into registers (CH stages per batch, the next batch
+// in flight while this one is multiplied), and the 8 partial int32
+// accumulators are summed exactly through LDS before the scale epilogue.
+// Operand layout per stage as in the tiled kernels: lane (li, lg) holds words
+// 4lg .. 4lg + 3 of row li (A) or column li (B).
+// ---------------------------------------------------------------------------
+template <int MT, bool B_NK, class OT>
+struct SkinnyCfg {
+  // stages per batch (two batches in registers). Measured at 16 x 4096 x
+  // 14336: 4 is best; 8 and 16 stages per batch were 15 % and 80 % slower.
+  static constexpr int CH = 4;
+};
+
+template <int MT, bool B_NK, class OT>
+__global__ void __launch_bounds__(512)
+gemm_i4_skinny(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
+               const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
+               typename OT::T* __restrict__ out, int64_t ldc, int M, int N, int K) {
+  constexpr int CH = SkinnyCfg<MT, B_NK, OT>::CH;
+  __shared__ __align__(16) v4i part[8][MT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int nk = K >> 7;
+  const int s_begin = wave * nk / 8, s_end = (wave + 1) * nk / 8;
+
+  const int n = min(n0 + li, N - 1);
+  const int32_t* bcol = B_NK ? b + (int64_t)n * ldb + 4 * lg : b + (int64_t)(4 * lg) * ldb + n;
+  const int32_t* arow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) arow[mt] = a + (int64_t)min(16 * mt + li, M - 1) * lda + 4 * lg;
+
+  v4i acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+
+  // Loads of stage s (clamped into the slice, so every batch issues the same
+  // loads; stages past the slice end are loaded but not multiplied).
+  v4i bq[2][CH], aq[2][CH][MT];
+  auto load = [&](int s0, auto set) {
+    constexpr int P = decltype(set)::value;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int s = min(s0 + c, s_end - 1);
+      if constexpr (B_NK) {
+        bq[P][c] = *reinterpret_cast<const v4i*>(bcol + 16 * s);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bq[P][c][t] = bcol[(int64_t)(16 * s + t) * ldb];
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) aq[P][c][mt] = *reinterpret_cast<const v4i*>(arow[mt] + 16 * s);
+    }
+  };
+  auto compute = [&](int s0, auto set) {
+    constexpr int P = decltype(set)::value;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      if (s0 + c >= s_end) break;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const v4i fb = widen_pair(bq[P][c][2 * h], bq[P][c][2 * h + 1]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+              fb, widen_pair(aq[P][c][mt][2 * h], aq[P][c][mt][2 * h + 1]), acc[mt], 0, 0, 0);
+      }
+    }
+  };
+  if (s_begin < s_end) {
+    load(s_begin, std::integral_constant<int, 0>{});
+    for (int s0 = s_begin; s0 < s_end; s0 += 2 * CH) {
+      load(s0 + CH, std::integral_constant<int, 1>{});
+      compute(s0, std::integral_constant<int, 0>{});
+      if (s0 + CH >= s_end) break;
+      load(s0 + 2 * CH, std::integral_constant<int, 0>{});
+      compute(s0 + CH, std::integral_constant<int, 1>{});
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) part[wave][mt][lane] = acc[mt];
+  __syncthreads();
+
+  // Waves 0 .. MT-1 each finish one 16-row block: exact int32 sum of the 8
+  // slices, then (float(acc) * sa) * sb and one rounding, as the tiled kernels.
+  if (wave >= MT) return;
+  const int mt = wave;
+  v4i sum = part[0][mt][lane];
+#pragma unroll
+  for (int w = 1; w < 8; ++w) sum += part[w][mt][lane];
+  const int m = 16 * mt + li;
+  const int nc = n0 + 4 * lg;
+  if (m >= M || nc >= N) return;
+  using T = typename OT::T;
+  const float sam = load_scale(sa, sad, m);
+  T v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(sum[r] >> 8, sam, load_scale(sb, sbd, min(nc + r, N - 1))));
+  T* o = out + (int64_t)m * ldc + nc;
+  if (nc + 3 < N) {
+    if constexpr (sizeof(T) == 2) {
+      typedef short v4s __attribute__((ext_vector_type(4)));
+      v4s pk;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
+      *reinterpret_cast<v4s*>(o) = pk;
+    } else {
+      *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (nc + r < N) o[r] = v[r];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host dispatch.
 // ---------------------------------------------------------------------------
 
@@ -848,6 +969,34 @@ static void dispatch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_
     launch_dma<256, 256, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, M, N, K, stream);
 }
 
+// QO_GEMM_NO_SKINNY=1 sends small M to the tiled kernels (tests use it to
+// cross-check the two).
+static bool gemm_allow_skinny() {
+  const char* e = getenv("QO_GEMM_NO_SKINNY");
+  return !(e && e[0] == '1');
+}
+
+template <class OT>
+static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, bool b_nk, const void* sa,
+                          int sad, const void* sb, int sbd, void* out, int64_t ldc, int M, int N, int K,
+                          hipStream_t stream) {
+  const dim3 grid((unsigned)((N + 15) / 16));
+  using T = typename OT::T;
+  auto go = [&](auto mt, auto nk_layout) {
+    hipLaunchKernelGGL((gemm_i4_skinny<decltype(mt)::value, decltype(nk_layout)::value, OT>), grid, dim3(512), 0,
+                       stream, a, lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, M, N, K);
+  };
+  auto by_layout = [&](auto mt) {
+    if (b_nk) go(mt, std::true_type{});
+    else go(mt, std::false_type{});
+  };
+  const int mt = (M + 15) / 16;
+  if (mt == 1) by_layout(std::integral_constant<int, 1>{});
+  else if (mt == 2) by_layout(std::integral_constant<int, 2>{});
+  else if (mt == 3) by_layout(std::integral_constant<int, 3>{});
+  else by_layout(std::integral_constant<int, 4>{});
+}
+
 template <class OT>
 static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, int64_t bsn, const void* sa,
                      int sad, const void* sb, int sbd, void* out, int64_t ldc, int64_t M, int64_t N, int64_t K,
@@ -863,6 +1012,11 @@ static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bs
                        ((uintptr_t)out % (4 * sizeof(T)) == 0) && (ldc % 4 == 0);
   if (allow_fast && fits && aligned && (b_nk || b_kn)) {
     const int m = (int)M, n = (int)N, k = (int)K;
+    // decode shapes: the skinny kernel (columns x K-slices, B streamed once)
+    if (m <= 64 && k % 128 == 0 && k > 0 && gemm_allow_skinny()) {
+      launch_skinny<OT>(a, lda, b, ldb, b_nk, sa, sad, sb, sbd, out, ldc, m, n, k, stream);
+      return;
+    }
     // pipelined kernel: whole 128-deep stages; KN rows read as 16-byte column groups
     if (k % 128 == 0 && k > 0 && (b_nk || n % 4 == 0) && gemm_allow_dma()) {
       if (b_nk)

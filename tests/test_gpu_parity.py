@@ -323,6 +323,29 @@ def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, monkeypatch):
     assert torch.equal(out, out_old)
 
 
+# Decode shapes (M <= 64): the skinny kernel, every row-block count, K slices
+# of uneven length over the 8 waves (nk % 8 != 0, nk < 8), ragged N; checked
+# against the oracle and against the tiled kernel on the same inputs.
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 14336), (16, 4096, 14336), (7, 100, 128), (32, 36, 640),
+                                   (48, 520, 1152), (64, 64, 4096), (5, 8, 896)])
+@pytest.mark.parametrize("bview", [False, True])
+def test_gemm_skinny_bit_exact(gpu, m, n, k, bview, monkeypatch):
+    case = wl.gemm_case(m, n, k, seed=5 * m + n + k, b_transposed_view=bview)
+    _say(f"gemm skinny {m}x{n}x{k} bview={bview}")
+    a, b = case.a.to(gpu), case.b.to(gpu)
+    sa, sb = case.scale_a.to(gpu), case.scale_b.to(gpu)
+    out = capi.int4_gemm(a, b, sa, sb, out_dtype=torch.bfloat16)
+    acc = capi.int4_gemm(a, b, torch.ones(m, device=gpu), torch.ones(n, device=gpu), out_dtype=torch.float32)
+    monkeypatch.setenv("QO_GEMM_NO_SKINNY", "1")
+    out_tiled = capi.int4_gemm(a, b, sa, sb, out_dtype=torch.bfloat16)
+    monkeypatch.delenv("QO_GEMM_NO_SKINNY")
+    torch.cuda.synchronize()
+    assert torch.equal(acc.cpu().to(torch.int64), _gemm_ref_acc(case.a, case.b).to(torch.int64))
+    assert torch.equal(out.cpu(), oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b,
+                                                          out_dtype=torch.bfloat16))
+    assert torch.equal(out, out_tiled)
+
+
 @pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
 def test_gemm_scale_and_out_dtypes(gpu, sdt, odt):
