@@ -116,6 +116,30 @@ __device__ inline float mul_f16hi(uint32_t p, float r) {
   return d;
 }
 
+// LDS-DMA of 16 bytes per lane: lane l's bytes land at LDS address lds + 16 l
+// (lds is wave-uniform, passed in M0). Issued as inline assembly so the
+// compiler's wait insertion does not see an LDS write it cannot order: with
+// the builtin it falls back to waiting for every outstanding load before LDS
+// reads at control-flow joins. The kernel orders these copies itself with
+// explicit vmcnt waits and barriers; every other load stays visible to the
+// compiler, and its own vmcnt waits remain correct (extra outstanding loads
+// only make them stricter).
+__device__ inline void dma16(const void* src, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+// The same copy addressed as a wave-uniform 64-bit base (SGPRs) plus the
+// lane's 32-bit byte offset.
+__device__ inline void dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+
+// LDS byte address of a __shared__ object (the value M0 takes for LDS-DMA).
+template <class P>
+__device__ inline uint32_t lds_addr(P* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
 }  // namespace qo
 
 // Thread-local error message used by qo_last_error().

@@ -163,32 +163,24 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
 template <class DT>
 struct MfmaOps;
 
-// V: 8-element operands of the 16x16x32 MFMA; V4: 4-element operands of the
-// 16x16x16 MFMA, used for an odd trailing 16-deep slab of the second product
-// (lane group g then holds k = 4g .. 4g+3, the same rows as Z's accumulator).
+// V: 8-element operands of the 16x16x32 MFMA. An odd trailing 16-deep slab of
+// the second product (M / 16 odd) is a zero-padded 32-deep slab: elements 0..3
+// of lane group g hold k = 4g .. 4g+3 (the rows of Z's accumulator), elements
+// 4..7 of both operands are zero, which leaves the MFMA's sum unchanged. (The
+// 16x16x16 MFMA gave wrong results in that role on gfx950.)
 template <>
 struct MfmaOps<F16T> {
   using V = v8h;
-  using V4 = v4h;
   __device__ static inline v4f mfma(V a, V b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  __device__ static inline v4f mfma16(V4 a, V4 b, v4f c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
   }
 };
 
 template <>
 struct MfmaOps<BF16T> {
   using V = v8bf;
-  using V4 = v4bf;
   __device__ static inline v4f mfma(V a, V b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  __device__ static inline v4f mfma16(V4 a, V4 b, v4f c) {
-    typedef short v4s __attribute__((ext_vector_type(4)));
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, a), __builtin_bit_cast(v4s, b), c, 0,
-                                                     0, 0);
   }
 };
 
@@ -353,7 +345,6 @@ __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 template <class DT, int MB, int NP, bool PACK>
 __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FqShape<MB, NP>::KS2 + 1],
-    const typename MfmaOps<DT>::V4 (&lt)[MB],
     const typename MfmaOps<DT>::V (&rf)[2][FqShape<MB, NP>::KS1], float (*red)[NP][2], int64_t t,
     int64_t tokens, float clip, void* __restrict__ out_codes, float* __restrict__ out_scales, int lane,
     int tau, int q) {
@@ -365,9 +356,8 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
   const int li = lane & 15, lg = lane >> 4;
 
   // First product, one 16-row block of Z at a time: Z[rb] = X[rb] R[:, pair].
-  using V4 = typename Ops::V4;
-  V zp[2][KS2 + 1];   // full 32-deep slabs of Z^T (one spare entry keeps the array non-empty)
-  V4 zt[2];           // odd trailing 16-row block of Z, when M / 16 is odd
+  constexpr int KSL = KS2 + (S::TAIL ? 1 : 0);   // slabs incl. the zero-padded tail
+  V zp[2][KS2 + 1];   // 32-deep slabs of Z^T
 #pragma unroll
   for (int rb = 0; rb < MB; ++rb) {
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
@@ -380,12 +370,11 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     // Rounding point 1, and the accumulator -> A-operand hand-off.
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      zp[0][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc0[r]);
+      zp[1][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc1[r]);
       if (S::TAIL && rb == MB - 1) {
-        zt[0][r] = DT::from_f(acc0[r]);
-        zt[1][r] = DT::from_f(acc1[r]);
-      } else {
-        zp[0][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc0[r]);
-        zp[1][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc1[r]);
+        zp[0][rb >> 1][4 + r] = DT::from_f(0.0f);
+        zp[1][rb >> 1][4 + r] = DT::from_f(0.0f);
       }
     }
     // keep the scheduler from hoisting every row block's fragment loads at once
@@ -401,13 +390,9 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
   for (int mb = 0; mb < MB; ++mb) {
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < KS2; ++s) {
+    for (int s = 0; s < KSL; ++s) {
       acc0 = Ops::mfma(zp[0][s], lf[mb][s], acc0);
       acc1 = Ops::mfma(zp[1][s], lf[mb][s], acc1);
-    }
-    if (S::TAIL) {
-      acc0 = Ops::mfma16(zt[0], lt[mb], acc0);
-      acc1 = Ops::mfma16(zt[1], lt[mb], acc1);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -554,7 +539,8 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   // copies, then gathered into B-operand fragments of the second product held
   // in VGPRs: lf[mb][s][j] = L[m'][m], m = 16mb + li,
   // m' = 32s + 16(j/4) + 4lg + j%4 — the row order of Z's accumulator pairs —
-  // and, for odd M/16, lt[mb][j] = L[16(MB-1) + 4lg + j][m].
+  // and, for odd M/16, the zero-padded slab lf[mb][KS2][j] = L[16(MB-1) + 4lg + j][m]
+  // for j < 4.
   {
     constexpr int CHUNKS = M * M / 8;   // 16-byte chunks of L
     typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -571,31 +557,30 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
     }
   }
   lds_barrier();
-  using V4 = typename MfmaOps<DT>::V4;
   V lf[MB][KS2 + 1];
-  V4 lt[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
     for (int s = 0; s < KS2; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) lf[mb][s][j] = xbuf1[(32 * s + 16 * (j >> 2) + 4 * lg + (j & 3)) * M + 16 * mb + li];
-    // trailing 16-deep slab: m' = 16(MB-1) + 4lg + j
+    // zero-padded trailing slab: m' = 16(MB-1) + 4lg + j for j < 4
 #pragma unroll
-    for (int j = 0; j < 4; ++j) lt[mb][j] = xbuf1[(S::TAIL ? 16 * (MB - 1) + 4 * lg + j : 0) * M + 16 * mb + li];
+    for (int j = 0; j < 8; ++j)
+      lf[mb][KS2][j] = (S::TAIL && j < 4) ? xbuf1[(16 * (MB - 1) + 4 * lg + j) * M + 16 * mb + li] : DT::from_f(0.0f);
   }
   lds_barrier();   // xbuf1 is free again for the first prefetch
 
   while (g < ngroups) {
     int64_t gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf1);
-    fq_mfma_group<DT, MB, NP, PACK>(xbuf0 + tau * S::XFRAGS * 512, lf, lt, rf, red, g * S::TPB + tau, tokens, clip,
+    fq_mfma_group<DT, MB, NP, PACK>(xbuf0 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
                                     out_codes, out_scales, lane, tau, q);
     g = gn;
     if (g >= ngroups) break;
     gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf0);
-    fq_mfma_group<DT, MB, NP, PACK>(xbuf1 + tau * S::XFRAGS * 512, lf, lt, rf, red, g * S::TPB + tau, tokens, clip,
+    fq_mfma_group<DT, MB, NP, PACK>(xbuf1 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
                                     out_codes, out_scales, lane, tau, q);
     g = gn;
   }
@@ -943,6 +928,279 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 }
 
 // ---------------------------------------------------------------------------
+// Pair kernel (fq_duo_kernel): N = 128, M = 16*MB (MB <= 8), the wide
+// transforms (e.g. 112 x 128 for 14336 features). Two waves share a token,
+// one per 64-column half c; the pair is the workgroup, and it walks the
+// tokens (persistent). R's fragments, Z and Y of a 64-column half take about
+// 180 registers, so the waves run one per SIMD (512 registers each), two
+// workgroups per CU.
+//
+// * X: each token's fragments arrive by LDS-DMA in A-operand order (lane l of
+//   fragment (rb, ks) holds X[16rb + l%16][32ks + 8(l/16) .. +7]); the DMA of
+//   the next token is issued as soon as both waves of the pair have read the
+//   current one, so it overlaps the second product and the epilogue.
+// * R: this wave's 64 columns as B-operand fragments in VGPRs (64 registers),
+//   in the column order of the wave kernel, so each lane ends up with whole
+//   adjacent code words.
+// * L: B-operand fragments of the second product in LDS, built once per
+//   workgroup and read by both waves of every pair.
+// * Products and rounding points as in fq_wave_kernel; the second product runs
+//   transposed with Z's accumulators as its A operand. When M / 16 is odd its
+//   last 16 rows of k form a zero-padded 32-deep slab (elements 4..7 of both
+//   operands zero; the MFMA's sum is unchanged), not a 16x16x16 MFMA, whose
+//   results here came out wrong on gfx950. max |Y| of the raw
+//   accumulators (rounding is monotonic and symmetric) is combined across the
+//   pair through LDS, then the scale, codes and packing of fq_wave_kernel.
+// ---------------------------------------------------------------------------
+template <int MB>
+struct DuoShape {
+  static constexpr int M = 16 * MB, N = 128, F = M * N;
+  static constexpr int KS1 = N / 32;           // 32-deep slabs of the first product (k = n')
+  static constexpr int KS2 = MB / 2;           // full 32-deep slabs of the second (k = m')
+  static constexpr bool TAIL = (MB & 1) != 0;  // one 16-deep slab when M / 16 is odd
+  static constexpr int XF = MB * KS1;          // 1 KiB X fragments per token
+  static constexpr int X_BYTES = XF * 1024;
+  static constexpr int KSL = KS2 + (TAIL ? 1 : 0);   // slabs incl. the zero-padded tail
+  static constexpr int LF_BYTES = MB * KSL * 1024;     // L fragments
+  // LDS block: X area + L fragments, at least R's N*N elements (set-up staging)
+  static constexpr int LDS_BYTES = X_BYTES + LF_BYTES > N * N * 2 ? X_BYTES + LF_BYTES : N * N * 2;
+  static_assert(MB >= 2 && MB <= 8, "M = 32 .. 128");
+  static_assert(XF % 2 == 0, "X fragments split over the pair");
+};
+
+template <class DT, int MB, bool PACK>
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
+fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+              const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
+              void* __restrict__ out_codes, float* __restrict__ out_scales) {
+  using S = DuoShape<MB>;
+  using T = typename DT::T;
+  using Ops = MfmaOps<DT>;
+  using V = typename Ops::V;
+  using Epi = FqEpi<DT>;
+  constexpr int M = S::M, N = S::N, F = S::F, KS1 = S::KS1, KS2 = S::KS2;
+  // one LDS block: the X area, then the L fragments (the set-up stages R
+  // across both)
+  __shared__ __align__(16) unsigned char lds_all[S::LDS_BYTES];
+  __shared__ float red[2];
+  unsigned char* const xs = lds_all;
+  unsigned char* const lfs = lds_all + S::X_BYTES;
+
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = wave;   // column half
+  const int64_t stride = gridDim.x;
+  unsigned char* const xslot = xs;
+
+  // LDS-DMA of token tt's X into this pair's slot: this wave copies fragments
+  // c, c + 2, c + 4, ... Slots past the last token re-read a valid row and
+  // store nothing.
+  auto issue_x = [&](int64_t tt) {
+    tt = tt < tokens ? tt : tokens - 1;
+    const T* base = x + tt * x_ld + li * N + 8 * lg;
+    const uint32_t lbase = lds_addr(xslot);
+#pragma unroll
+    for (int i = 0; i < S::XF / 2; ++i) {
+      const int f = c + 2 * i;
+      dma16(base + (f / KS1) * 16 * N + 32 * (f % KS1), lbase + f * 1024);
+    }
+  };
+
+  // Set-up, once per workgroup. L and R are copied row-major into LDS by
+  // LDS-DMA (coalesced 16-byte chunks), then rearranged into fragments from
+  // LDS: R first (N*N elements, over the X area and the L-fragment area) into
+  // this wave's registers, then L (over the X area) into the L fragments.
+  static_assert(M * M * 2 <= S::X_BYTES, "L staging space");
+  auto stage_rows = [&](const T* src, int chunks) {   // chunk c (8 elements) -> lds_all + 16 c
+    const uint32_t lb = lds_addr(lds_all);
+#pragma unroll 1
+    for (int c0 = wave * 64; c0 < chunks; c0 += 128)
+      if (c0 + lane < chunks) dma16(src + 8 * (c0 + lane), lb + 16 * c0);
+    wait_vmcnt<0>();
+    lds_barrier();
+  };
+  stage_rows(right, N * N / 8);
+  // R fragments of this wave's columns: rf[q][h][ks][j] = R[32ks + 8lg + j][n],
+  // n = 64c + 16(li/4) + 8q + 4h + li%4.
+  V rf[2][2][KS1];
+  {
+    const T* rs = reinterpret_cast<const T*>(lds_all);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int n = 64 * c + 16 * (li >> 2) + 8 * q + 4 * h + (li & 3);
+#pragma unroll
+        for (int ks = 0; ks < KS1; ++ks)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) rf[q][h][ks][j] = rs[(32 * ks + 8 * lg + j) * N + n];
+      }
+  }
+  lds_barrier();   // R is in registers; the staging space is free
+  stage_rows(left, M * M / 8);
+  // L fragments (16 bytes per lane and slab): slab (mb, s), lane l, element j
+  // holds L[32s + 16(j/4) + 4(l/16) + j%4][16mb + l%16]; in the zero-padded
+  // tail slab (s = KS2, M / 16 odd) elements 4..7 are zero.
+  {
+    const T* ls = reinterpret_cast<const T*>(lds_all);
+#pragma unroll 1
+    for (int fr = wave; fr < MB * S::KSL; fr += 2) {
+      const int mb = fr / S::KSL, sl = fr % S::KSL;
+      const int m = 16 * mb + li;
+      V v;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int mp = 32 * sl + 16 * (jj >> 2) + 4 * lg + (jj & 3);
+        v[jj] = (sl == KS2 && jj >= 4) ? DT::from_f(0.0f) : ls[mp * M + m];
+      }
+      *reinterpret_cast<V*>(lfs + fr * 1024 + 16 * lane) = v;
+    }
+  }
+  lds_barrier();   // L fragments written, the stage (X area) is free
+  issue_x(blockIdx.x);
+
+  for (int64_t t = blockIdx.x; t < tokens; t += stride) {
+    wait_vmcnt<0>();   // this wave's share of X (and the last epilogue's stores)
+    lds_barrier();     // the pair's X (and, the first time, the L fragments) visible
+
+    // First product Z = X R for this wave's 64 columns, rounding point 1, the
+    // accumulators packed as A operands of the second product:
+    //   zp[q][h][s][4e + r] = Z[16(2s + e) + 4lg + r][n(q, h, li)], zt for the tail.
+    V zp[2][2][S::KSL];
+    // X fragments one row block ahead; the scheduling barriers keep the
+    // compiler from hoisting every block's reads (their registers would not
+    // fit next to R's fragments and Z)
+    V xa[2][KS1];
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks) xa[0][ks] = *reinterpret_cast<const V*>(xslot + ks * 1024 + 16 * lane);
+#pragma unroll
+    for (int rb = 0; rb < MB; ++rb) {
+      if (rb + 1 < MB) {
+#pragma unroll
+        for (int ks = 0; ks < KS1; ++ks)
+          xa[(rb + 1) & 1][ks] = *reinterpret_cast<const V*>(xslot + ((rb + 1) * KS1 + ks) * 1024 + 16 * lane);
+      }
+      const V (&a)[KS1] = xa[rb & 1];
+      v4f acc[2][2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          acc[q][h] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS1; ++ks) acc[q][h] = Ops::mfma(a[ks], rf[q][h][ks], acc[q][h]);
+        }
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            zp[q][h][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc[q][h][r]);
+            if (S::TAIL && rb == MB - 1) zp[q][h][rb >> 1][4 + r] = DT::from_f(0.0f);
+          }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_barrier();                 // both waves are done with X
+    issue_x(t + stride);           // next token's X lands during the rest of this one
+
+    // Second product, transposed, rounding point 2. Lane (li, lg) of block
+    // (mb, q) holds Y[16mb + li][64c + 8(2lg + q) + 4h + r]: packed word
+    // 8c + 2lg + q of row 16mb + li, nibbles r (h = 0) and r + 4 (h = 1).
+    uint32_t yp[MB][2][4];
+    float amax = 0.f;
+    // L fragments one row block ahead (same reason as X above)
+    V lfb[2][S::KSL];
+    auto load_l = [&](int mb, int buf) {
+#pragma unroll
+      for (int s = 0; s < S::KSL; ++s)
+        lfb[buf][s] = *reinterpret_cast<const V*>(lfs + (mb * S::KSL + s) * 1024 + 16 * lane);
+    };
+    load_l(0, 0);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      if (mb + 1 < MB) load_l(mb + 1, (mb + 1) & 1);
+      const V (&lf)[S::KSL] = lfb[mb & 1];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        v4f acc[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          acc[h] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < S::KSL; ++s) acc[h] = Ops::mfma(zp[q][h][s], lf[s], acc[h]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          yp[mb][q][r] = Epi::pack(acc[0][r], acc[1][r]);
+          amax = fmaxf(fmaxf(amax, fabsf(acc[0][r])), fabsf(acc[1][r]));
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // max |y| over the token: the wave, then the pair (non-negative floats
+    // order like their bit patterns)
+    amax = __builtin_bit_cast(float, wave_max_u32(__builtin_bit_cast(uint32_t, amax)));
+    if (lane == 0) red[c] = amax;
+    lds_barrier();
+    amax = DT::round(fmaxf(red[0], red[1]));
+    const float s = fq_scale_abs<DT>(amax, clip);
+    if (t < tokens) {
+      if (c == 0 && lane == 0) out_scales[t] = s;
+      if (PACK && s > 0.f) {
+        const float rcp = 1.0f / s;
+        int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + 8 * c + 2 * lg;
+        const bool low = DT::round(amax * rcp) > 8.5f;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const uint32_t w0 = low ? Epi::template word4<true>(yp[mb][0], rcp) : Epi::template word4<false>(yp[mb][0], rcp);
+          const uint32_t w1 = low ? Epi::template word4<true>(yp[mb][1], rcp) : Epi::template word4<false>(yp[mb][1], rcp);
+          *reinterpret_cast<v2i*>(orow + (16 * mb + li) * (N / 8)) = v2i{(int)w0, (int)w1};
+        }
+      } else {
+        // int8 codes, and tokens whose scale rounded to 0 (the fallback's 0/0 codes)
+        const float rcp = 1.0f / s;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const int m = 16 * mb + li;
+            int code[8];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float y0 = Epi::lo(yp[mb][q][r]), y1 = Epi::hi(yp[mb][q][r]);
+              if (s > 0.f) {
+                code[r] = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y0 * rcp, -8.0f, 7.0f)));
+                code[4 + r] = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y1 * rcp, -8.0f, 7.0f)));
+              } else {
+                code[r] = fq_code_from_quot<PACK>(DT::round(opaque(y0) / s));
+                code[4 + r] = fq_code_from_quot<PACK>(DT::round(opaque(y1) / s));
+              }
+            }
+            const int word = 8 * c + 2 * lg + q;
+            if (PACK) {
+              uint32_t w = 0;
+#pragma unroll
+              for (int j = 0; j < 8; ++j) w |= (uint32_t)(code[j] + 8) << (4 * j);
+              reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (N / 8) + word] = (int32_t)w;
+            } else {
+              uint32_t lo4 = 0, hi4 = 0;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                lo4 |= (uint32_t)(code[j] & 0xFF) << (8 * j);
+                hi4 |= (uint32_t)(code[4 + j] & 0xFF) << (8 * j);
+              }
+              *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + m * N + 8 * word) =
+                  v2i{(int)lo4, (int)hi4};
+            }
+          }
+      }
+    }
+  }
+  wait_vmcnt<0>();   // no LDS-DMA may still be writing when the workgroup retires
+}
+
+// ---------------------------------------------------------------------------
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
 
@@ -984,6 +1242,25 @@ static int launch_wave(const void* x, int64_t tokens, int64_t x_ld, const void* 
   return QO_OK;
 }
 
+template <class DT, int MB, bool PACK>
+static int launch_duo(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right, float clip,
+                      void* out_codes, float* out_scales, hipStream_t stream) {
+  using T = typename DT::T;
+  // two workgroups (four waves, one per SIMD) per CU
+  const int64_t grid = std::min<int64_t>(tokens, (int64_t)device_cu_count() * 2);
+  hipLaunchKernelGGL((fq_duo_kernel<DT, MB, PACK>), dim3((unsigned)grid), dim3(128), 0, stream,
+                     reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
+                     reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
+  return QO_OK;
+}
+
+// QO_FQ_NO_DUO=1 keeps N = 128 shapes on fq_mfma_kernel (tests use it to
+// cross-check the two).
+static bool fq_allow_duo() {
+  const char* e = getenv("QO_FQ_NO_DUO");
+  return !(e && e[0] == '1');
+}
+
 // QO_FQ_NO_WAVE=1 keeps small shapes on fq_mfma_kernel (tests use it to
 // cross-check the two MFMA kernels).
 static bool fq_allow_wave() {
@@ -1007,6 +1284,17 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
     QO_FQ_WAVE_CASE(2, 1)   // 32 x 32 (hidden 1024)
     QO_FQ_WAVE_CASE(4, 1)   // 64 x 32 (hidden 2048)
 #undef QO_FQ_WAVE_CASE
+  }
+  // the pair kernel takes its scale from max |Y| as well
+  if (fq_allow_duo() && clip > 0.f && clip <= 3.4e38f && N == 128) {
+#define QO_FQ_DUO_CASE(MB_)                                                                                  \
+    if (M == 16 * (MB_))                                                                                     \
+      return launch_duo<DT, MB_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream);
+    QO_FQ_DUO_CASE(7)   // 112 x 128 (hidden 14336)
+    QO_FQ_DUO_CASE(4)   // 64 x 128  (hidden 8192)
+    QO_FQ_DUO_CASE(8)   // 128 x 128 (hidden 16384)
+    QO_FQ_DUO_CASE(6)   // 96 x 128  (hidden 12288)
+#undef QO_FQ_DUO_CASE
   }
 #define QO_FQ_CASE(MB_, NP_)                                                                      \
   if (M == 16 * (MB_) && N == 32 * (NP_))                                                         \

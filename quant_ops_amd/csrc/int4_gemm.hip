@@ -322,24 +322,6 @@ struct DmaStage {
   static_assert(B_NK || BN <= 256, "a KN row of the tile must fit one 1 KiB DMA");
 };
 
-// LDS-DMA of 16 bytes per lane: lane l's bytes land at LDS address lds + 16 l
-// (lds is wave-uniform, passed in M0). Issued as inline assembly so the
-// compiler's wait insertion does not see an LDS write it cannot order: with
-// the builtin it falls back to waiting for every outstanding load before LDS
-// reads at control-flow joins. The kernel orders these copies itself with
-// explicit vmcnt waits and barriers; every other load stays visible to the
-// compiler, and its own vmcnt waits remain correct (extra outstanding loads
-// only make them stricter).
-__device__ inline void dma16(const void* src, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
-}
-
-// The same copy addressed as a wave-uniform 64-bit base (SGPRs) plus the
-// lane's 32-bit byte offset.
-__device__ inline void dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
-}
-
 template <int N>
 __device__ inline void gemm_wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt out of range");

@@ -160,6 +160,26 @@ def test_quantize_wave_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack,
     assert torch.equal(s1, s2) and torch.equal(q1, q2)
 
 
+@pytest.mark.parametrize("pack", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mn", [(112, 128), (64, 128), (128, 128), (96, 128)])
+@pytest.mark.parametrize("tokens", [1, 37, 1030])
+def test_quantize_pair_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack, monkeypatch):
+    """The two-waves-per-token kernel (N = 128) and the workgroup kernel use the
+    same fragment layouts and k order, so their codes and scales agree bit for
+    bit; 1030 tokens make each workgroup loop over several tokens."""
+    m, n = mn
+    case = wl.quant_case("pair", tokens, m, n, dtype, 0.9, pack, seed=tokens + m, outlier_frac=0.005,
+                         outlier_scale=30.0)
+    case.x[tokens // 2].zero_()
+    _say(f"pair vs group kernel T={tokens} {m}x{n} {dtype} pack={pack}")
+    q1, s1 = run_capi_quant(case, gpu)
+    monkeypatch.setenv("QO_FQ_NO_DUO", "1")
+    q2, s2 = run_capi_quant(case, gpu)
+    monkeypatch.delenv("QO_FQ_NO_DUO")
+    assert torch.equal(s1, s2) and torch.equal(q1, q2)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mn", [(64, 64), (112, 128), (16, 16)])
 def test_quantize_matches_sequential_accumulation_oracle(gpu, dtype, mn, monkeypatch):
