@@ -18,6 +18,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -206,6 +207,13 @@ struct FqEpi<F16T> {
     const v2h h = {(_Float16)opaque(a), (_Float16)opaque(b)};
     return __builtin_bit_cast(uint32_t, h);
   }
+  // The same rounding of two MFMA accumulator values. An MFMA result has no
+  // product for the compiler to fuse into the conversion, so no opaque() is
+  // needed (which would copy accumulators that are read again for the absmax).
+  __device__ static inline uint32_t pack_acc(float a, float b) {
+    const v2h h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, h);
+  }
   __device__ static inline float lo(uint32_t p) { return (float)__builtin_bit_cast(v2h, p)[0]; }
   __device__ static inline float hi(uint32_t p) { return (float)__builtin_bit_cast(v2h, p)[1]; }
   // fp16: 1544 = 1536 + 8 has a unit ulp, so t + 1544 is the integer 1536 + q + 8,
@@ -266,6 +274,10 @@ struct FqEpi<BF16T> {
     const v2bf h = {(__bf16)opaque(a), (__bf16)opaque(b)};
     return __builtin_bit_cast(uint32_t, h);
   }
+  __device__ static inline uint32_t pack_acc(float a, float b) {
+    const v2bf h = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, h);
+  }
   __device__ static inline float lo(uint32_t p) { return __builtin_bit_cast(float, p << 16); }
   __device__ static inline float hi(uint32_t p) { return __builtin_bit_cast(float, p & 0xFFFF0000u); }
   // bf16: rounded pair back to float32, then + 12582920 = 1.5 * 2^23 + 8 leaves
@@ -290,6 +302,36 @@ struct FqEpi<BF16T> {
 #pragma unroll
     for (int r = 0; r < 4; ++r) accumulate(word, p[r], rcp, r);
     return word;
+  }
+
+  // The same word through byte packing: t = rnd(y * rcp) for the pair (one
+  // v_cvt_pk), the upper clamp on the packed pair as signed 16-bit integers
+  // (non-negative bf16 patterns order like their values, negative ones are
+  // negative integers, so min with 7.0's pattern clamps only t > 7), then
+  // v_cvt_pk_u8_f32 of t + 8 (exact) rounds half to even and saturates at 0,
+  // which is round-half-even of t and the lower clamp at -8, offset by 8.
+  // Even codes go to bytes of `ev`, odd codes to bytes of `od`; ev | od << 4
+  // puts code i in nibble i.
+  __device__ static inline uint32_t word_u8(const uint32_t (&p)[4], float rcp) {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    const v2s seven = {(short)0x40E0, (short)0x40E0};
+    uint32_t ev = 0u, od = 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      // one v_cvt_pk_bf16_f32 for the pair (written out: as two conversions
+      // feeding a 16-bit integer min, the compiler emits two converts and a
+      // v_perm). Its operands are VALU products, never MFMA results.
+      uint32_t tp;
+      asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(tp) : "v"(lo(p[r]) * rcp), "v"(hi(p[r]) * rcp));
+      v2s t = __builtin_bit_cast(v2s, tp);
+      t = __builtin_elementwise_min(t, seven);
+      const uint32_t tb = __builtin_bit_cast(uint32_t, t);
+      const float f0 = lo(tb) + 8.0f, f1 = hi(tb) + 8.0f;   // codes r and r + 4
+      uint32_t& d = (r & 1) ? od : ev;
+      d = __builtin_amdgcn_cvt_pk_u8_f32(f0, r >> 1, d);
+      d = __builtin_amdgcn_cvt_pk_u8_f32(f1, 2 + (r >> 1), d);
+    }
+    return ev | (od << 4);
   }
 
   // max |y| of rounded Y pairs as a 16-bit pattern (sign-cleared bf16 bits
@@ -959,17 +1001,33 @@ struct DuoShape {
   static constexpr int KS2 = MB / 2;           // full 32-deep slabs of the second (k = m')
   static constexpr bool TAIL = (MB & 1) != 0;  // one 16-deep slab when M / 16 is odd
   static constexpr int XF = MB * KS1;          // 1 KiB X fragments per token
-  static constexpr int X_BYTES = XF * 1024;
+  static constexpr int X_BYTES = XF * 1024;    // one X buffer
   static constexpr int KSL = KS2 + (TAIL ? 1 : 0);   // slabs incl. the zero-padded tail
   static constexpr int LF_BYTES = MB * KSL * 1024;     // L fragments
+  static constexpr int SLOTS = 2;              // token pairs per workgroup (four waves)
+  // X buffers per slot: two (the next-but-one token's X is copied while this
+  // one is processed) where the LDS holds them, else one
+  static constexpr int XB = SLOTS * 2 * X_BYTES + LF_BYTES + 64 <= 160 * 1024 ? 2 : 1;
+  static constexpr int XAREA = SLOTS * XB * X_BYTES;
   // LDS block: X area + L fragments, at least R's N*N elements (set-up staging)
-  static constexpr int LDS_BYTES = X_BYTES + LF_BYTES > N * N * 2 ? X_BYTES + LF_BYTES : N * N * 2;
+  static constexpr int LDS_BYTES = XAREA + LF_BYTES > N * N * 2 ? XAREA + LF_BYTES : N * N * 2;
   static_assert(MB >= 2 && MB <= 8, "M = 32 .. 128");
   static_assert(XF % 2 == 0, "X fragments split over the pair");
 };
 
+// s_waitcnt vmcnt(n) for a wave-uniform runtime n: the largest of a few fixed
+// levels not above n (a smaller count is a stricter wait).
+template <int A, int B, int C>
+__device__ inline void wait_vmcnt_at_most(int n) {
+  static_assert(A < B && B < C, "levels ascending");
+  if (n >= C) wait_vmcnt<C>();
+  else if (n >= B) wait_vmcnt<B>();
+  else if (n >= A) wait_vmcnt<A>();
+  else wait_vmcnt<0>();
+}
+
 template <class DT, int MB, bool PACK>
-__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(128 * DuoShape<MB>::SLOTS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
               const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
               void* __restrict__ out_codes, float* __restrict__ out_scales) {
@@ -978,27 +1036,29 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   using Ops = MfmaOps<DT>;
   using V = typename Ops::V;
   using Epi = FqEpi<DT>;
-  constexpr int M = S::M, N = S::N, F = S::F, KS1 = S::KS1, KS2 = S::KS2;
-  // one LDS block: the X area, then the L fragments (the set-up stages R
+  constexpr int M = S::M, N = S::N, F = S::F, KS1 = S::KS1, KS2 = S::KS2, XB = S::XB, SLOTS = S::SLOTS;
+  // one LDS block: the X buffers, then the L fragments (the set-up stages R
   // across both)
   __shared__ __align__(16) unsigned char lds_all[S::LDS_BYTES];
-  __shared__ float red[2];
-  unsigned char* const xs = lds_all;
-  unsigned char* const lfs = lds_all + S::X_BYTES;
+  __shared__ float red[SLOTS][2];
+  unsigned char* const lfs = lds_all + S::XAREA;
 
   const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int c = wave;   // column half
-  const int64_t stride = gridDim.x;
-  unsigned char* const xslot = xs;
+  const int p = wave >> 1, c = wave & 1;   // token slot, column half
+  unsigned char* const xslot = lds_all + p * XB * S::X_BYTES;
+  // token of this wave's slot in iteration it
+  const int64_t step = (int64_t)gridDim.x * SLOTS;
+  const int64_t t0 = (int64_t)blockIdx.x * SLOTS + p;
 
-  // LDS-DMA of token tt's X into this pair's slot: this wave copies fragments
-  // c, c + 2, c + 4, ... Slots past the last token re-read a valid row and
-  // store nothing.
-  auto issue_x = [&](int64_t tt) {
+  // LDS-DMA of token tt's X into buffer b of this slot: this wave copies
+  // fragments c, c + 2, c + 4, ... (lane l of fragment (rb, ks) holds
+  // X[16rb + l%16][32ks + 8(l/16) .. +7]). Tokens past the last re-read a valid
+  // row and store nothing.
+  auto issue_x = [&](int64_t tt, int b) {
     tt = tt < tokens ? tt : tokens - 1;
     const T* base = x + tt * x_ld + li * N + 8 * lg;
-    const uint32_t lbase = lds_addr(xslot);
+    const uint32_t lbase = lds_addr(xslot + b * S::X_BYTES);
 #pragma unroll
     for (int i = 0; i < S::XF / 2; ++i) {
       const int f = c + 2 * i;
@@ -1008,13 +1068,13 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
 
   // Set-up, once per workgroup. L and R are copied row-major into LDS by
   // LDS-DMA (coalesced 16-byte chunks), then rearranged into fragments from
-  // LDS: R first (N*N elements, over the X area and the L-fragment area) into
-  // this wave's registers, then L (over the X area) into the L fragments.
-  static_assert(M * M * 2 <= S::X_BYTES, "L staging space");
+  // LDS: R first (N*N elements) into this wave's registers, then L (over the
+  // X area) into the L fragments.
+  static_assert(M * M * 2 <= S::XAREA, "L staging space");
   auto stage_rows = [&](const T* src, int chunks) {   // chunk c (8 elements) -> lds_all + 16 c
     const uint32_t lb = lds_addr(lds_all);
 #pragma unroll 1
-    for (int c0 = wave * 64; c0 < chunks; c0 += 128)
+    for (int c0 = wave * 64; c0 < chunks; c0 += 64 * 2 * SLOTS)
       if (c0 + lane < chunks) dma16(src + 8 * (c0 + lane), lb + 16 * c0);
     wait_vmcnt<0>();
     lds_barrier();
@@ -1044,43 +1104,47 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   {
     const T* ls = reinterpret_cast<const T*>(lds_all);
 #pragma unroll 1
-    for (int fr = wave; fr < MB * S::KSL; fr += 2) {
+    for (int fr = wave; fr < MB * S::KSL; fr += 2 * SLOTS) {
       const int mb = fr / S::KSL, sl = fr % S::KSL;
       const int m = 16 * mb + li;
       V v;
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
         const int mp = 32 * sl + 16 * (jj >> 2) + 4 * lg + (jj & 3);
-        v[jj] = (sl == KS2 && jj >= 4) ? DT::from_f(0.0f) : ls[mp * M + m];
+        v[jj] = (sl == KS2 && jj >= 4) ? __builtin_bit_cast(T, (short)0) : ls[mp * M + m];
       }
       *reinterpret_cast<V*>(lfs + fr * 1024 + 16 * lane) = v;
     }
   }
-  lds_barrier();   // L fragments written, the stage (X area) is free
-  issue_x(blockIdx.x);
+  lds_barrier();   // L fragments written, the X area is free
+#pragma unroll
+  for (int b = 0; b < XB; ++b) issue_x(t0 + b * step, b);
 
-  for (int64_t t = blockIdx.x; t < tokens; t += stride) {
-    wait_vmcnt<0>();   // this wave's share of X (and the last epilogue's stores)
-    lds_barrier();     // the pair's X (and, the first time, the L fragments) visible
+  // Stores this wave issued in the last XB iterations (the output stores sit
+  // between the copies the next waits target, so the wait counts them).
+  constexpr int STORES = MB;   // output stores per wave and valid token (+1 scale store for c == 0)
+  int st_prev[XB] = {};
+  for (int64_t it = 0; t0 - p + it * step < tokens; ++it) {
+    const int64_t t = t0 + it * step;
+    const int b = XB == 2 ? (int)(it & 1) : 0;
+    unsigned char* const xb = xslot + b * S::X_BYTES;
+    // this iteration's copy is older than: the stores of the last XB
+    // iterations and the copies issued in the last XB - 1
+    int newer = (XB - 1) * (S::XF / 2);
+#pragma unroll
+    for (int k = 0; k < XB; ++k) newer += st_prev[k];
+    wait_vmcnt_at_most<S::XF / 2, S::XF / 2 + STORES, S::XF / 2 + 2 * STORES>(newer);
+    lds_barrier();   // the slot's X (and, the first time, the L fragments) visible
 
     // First product Z = X R for this wave's 64 columns, rounding point 1, the
     // accumulators packed as A operands of the second product:
-    //   zp[q][h][s][4e + r] = Z[16(2s + e) + 4lg + r][n(q, h, li)], zt for the tail.
+    //   zp[q][h][s][4e + r] = Z[16(2s + e) + 4lg + r][n(q, h, li)].
     V zp[2][2][S::KSL];
-    // X fragments one row block ahead; the scheduling barriers keep the
-    // compiler from hoisting every block's reads (their registers would not
-    // fit next to R's fragments and Z)
-    V xa[2][KS1];
-#pragma unroll
-    for (int ks = 0; ks < KS1; ++ks) xa[0][ks] = *reinterpret_cast<const V*>(xslot + ks * 1024 + 16 * lane);
 #pragma unroll
     for (int rb = 0; rb < MB; ++rb) {
-      if (rb + 1 < MB) {
+      V a[KS1];
 #pragma unroll
-        for (int ks = 0; ks < KS1; ++ks)
-          xa[(rb + 1) & 1][ks] = *reinterpret_cast<const V*>(xslot + ((rb + 1) * KS1 + ks) * 1024 + 16 * lane);
-      }
-      const V (&a)[KS1] = xa[rb & 1];
+      for (int ks = 0; ks < KS1; ++ks) a[ks] = *reinterpret_cast<const V*>(xb + (rb * KS1 + ks) * 1024 + 16 * lane);
       v4f acc[2][2];
 #pragma unroll
       for (int q = 0; q < 2; ++q)
@@ -1096,31 +1160,23 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            zp[q][h][rb >> 1][(rb & 1) * 4 + r] = DT::from_f(acc[q][h][r]);
-            if (S::TAIL && rb == MB - 1) zp[q][h][rb >> 1][4 + r] = DT::from_f(0.0f);
+            zp[q][h][rb >> 1][(rb & 1) * 4 + r] = (T)acc[q][h][r];   // an MFMA result: no opaque()
+            if (S::TAIL && rb == MB - 1) zp[q][h][rb >> 1][4 + r] = __builtin_bit_cast(T, (short)0);
           }
-      __builtin_amdgcn_sched_barrier(0);
     }
-    lds_barrier();                 // both waves are done with X
-    issue_x(t + stride);           // next token's X lands during the rest of this one
+    lds_barrier();                     // both waves of each pair are done with buffer b
+    issue_x(t + XB * step, b);         // the token XB iterations ahead
 
     // Second product, transposed, rounding point 2. Lane (li, lg) of block
     // (mb, q) holds Y[16mb + li][64c + 8(2lg + q) + 4h + r]: packed word
     // 8c + 2lg + q of row 16mb + li, nibbles r (h = 0) and r + 4 (h = 1).
     uint32_t yp[MB][2][4];
     float amax = 0.f;
-    // L fragments one row block ahead (same reason as X above)
-    V lfb[2][S::KSL];
-    auto load_l = [&](int mb, int buf) {
-#pragma unroll
-      for (int s = 0; s < S::KSL; ++s)
-        lfb[buf][s] = *reinterpret_cast<const V*>(lfs + (mb * S::KSL + s) * 1024 + 16 * lane);
-    };
-    load_l(0, 0);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      if (mb + 1 < MB) load_l(mb + 1, (mb + 1) & 1);
-      const V (&lf)[S::KSL] = lfb[mb & 1];
+      V lf[S::KSL];
+#pragma unroll
+      for (int sl = 0; sl < S::KSL; ++sl) lf[sl] = *reinterpret_cast<const V*>(lfs + (mb * S::KSL + sl) * 1024 + 16 * lane);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         v4f acc[2];
@@ -1128,72 +1184,94 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
         for (int h = 0; h < 2; ++h) {
           acc[h] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int s = 0; s < S::KSL; ++s) acc[h] = Ops::mfma(zp[q][h][s], lf[s], acc[h]);
+          for (int sl = 0; sl < S::KSL; ++sl) acc[h] = Ops::mfma(zp[q][h][sl], lf[sl], acc[h]);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          yp[mb][q][r] = Epi::pack(acc[0][r], acc[1][r]);
+          yp[mb][q][r] = Epi::pack_acc(acc[0][r], acc[1][r]);
           amax = fmaxf(fmaxf(amax, fabsf(acc[0][r])), fabsf(acc[1][r]));
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
     // max |y| over the token: the wave, then the pair (non-negative floats
     // order like their bit patterns)
     amax = __builtin_bit_cast(float, wave_max_u32(__builtin_bit_cast(uint32_t, amax)));
-    if (lane == 0) red[c] = amax;
+    if (lane == 0) red[p][c] = amax;
     lds_barrier();
-    amax = DT::round(fmaxf(red[0], red[1]));
+    amax = DT::round(fmaxf(red[p][0], red[p][1]));
     const float s = fq_scale_abs<DT>(amax, clip);
-    if (t < tokens) {
-      if (c == 0 && lane == 0) out_scales[t] = s;
-      if (PACK && s > 0.f) {
-        const float rcp = 1.0f / s;
-        int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + 8 * c + 2 * lg;
-        const bool low = DT::round(amax * rcp) > 8.5f;
+
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const uint32_t w0 = low ? Epi::template word4<true>(yp[mb][0], rcp) : Epi::template word4<false>(yp[mb][0], rcp);
-          const uint32_t w1 = low ? Epi::template word4<true>(yp[mb][1], rcp) : Epi::template word4<false>(yp[mb][1], rcp);
-          *reinterpret_cast<v2i*>(orow + (16 * mb + li) * (N / 8)) = v2i{(int)w0, (int)w1};
+    for (int k = XB - 1; k > 0; --k) st_prev[k] = st_prev[k - 1];
+    st_prev[0] = 0;
+    if (t < tokens) {
+      // exactly STORES output stores (one per 16-row block), plus the scale
+      st_prev[0] = STORES + (c == 0 ? 1 : 0);
+      if (c == 0 && lane == 0) out_scales[t] = s;
+      const float rcp = 1.0f / s;
+      if (PACK) {
+        int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + 8 * c + 2 * lg;
+        if (s > 0.f) {
+          if constexpr (std::is_same<DT, BF16T>::value) {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+              *reinterpret_cast<v2i*>(orow + (16 * mb + li) * (N / 8)) =
+                  v2i{(int)Epi::word_u8(yp[mb][0], rcp), (int)Epi::word_u8(yp[mb][1], rcp)};
+          } else if (DT::round(amax * rcp) > 8.5f) {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+              *reinterpret_cast<v2i*>(orow + (16 * mb + li) * (N / 8)) =
+                  v2i{(int)Epi::template word4<true>(yp[mb][0], rcp), (int)Epi::template word4<true>(yp[mb][1], rcp)};
+          } else {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+              *reinterpret_cast<v2i*>(orow + (16 * mb + li) * (N / 8)) =
+                  v2i{(int)Epi::template word4<false>(yp[mb][0], rcp), (int)Epi::template word4<false>(yp[mb][1], rcp)};
+          }
+        } else {
+          // scale rounded to 0 (an all-zero fp16 token): the fallback's 0/0 codes
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+            uint32_t w[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              w[q] = 0;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                w[q] |= (uint32_t)(fq_code_from_quot<true>(DT::round(opaque(Epi::lo(yp[mb][q][r])) / s)) + 8) << (4 * r);
+                w[q] |= (uint32_t)(fq_code_from_quot<true>(DT::round(opaque(Epi::hi(yp[mb][q][r])) / s)) + 8)
+                        << (4 * r + 16);
+              }
+            }
+            *reinterpret_cast<v2i*>(orow + (16 * mb + li) * (N / 8)) = v2i{(int)w[0], (int)w[1]};
+          }
         }
       } else {
-        // int8 codes, and tokens whose scale rounded to 0 (the fallback's 0/0 codes)
-        const float rcp = 1.0f / s;
+        // int8 codes: 16 bytes per row block (words 8c + 2lg and + 1)
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+        for (int mb = 0; mb < MB; ++mb) {
+          uint32_t lo4[2], hi4[2];
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
-            const int m = 16 * mb + li;
-            int code[8];
+            lo4[q] = hi4[q] = 0;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const float y0 = Epi::lo(yp[mb][q][r]), y1 = Epi::hi(yp[mb][q][r]);
+              int c0, c1;
               if (s > 0.f) {
-                code[r] = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y0 * rcp, -8.0f, 7.0f)));
-                code[4 + r] = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y1 * rcp, -8.0f, 7.0f)));
+                c0 = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y0 * rcp, -8.0f, 7.0f)));
+                c1 = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y1 * rcp, -8.0f, 7.0f)));
               } else {
-                code[r] = fq_code_from_quot<PACK>(DT::round(opaque(y0) / s));
-                code[4 + r] = fq_code_from_quot<PACK>(DT::round(opaque(y1) / s));
+                c0 = fq_code_from_quot<false>(DT::round(opaque(y0) / s));
+                c1 = fq_code_from_quot<false>(DT::round(opaque(y1) / s));
               }
-            }
-            const int word = 8 * c + 2 * lg + q;
-            if (PACK) {
-              uint32_t w = 0;
-#pragma unroll
-              for (int j = 0; j < 8; ++j) w |= (uint32_t)(code[j] + 8) << (4 * j);
-              reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (N / 8) + word] = (int32_t)w;
-            } else {
-              uint32_t lo4 = 0, hi4 = 0;
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                lo4 |= (uint32_t)(code[j] & 0xFF) << (8 * j);
-                hi4 |= (uint32_t)(code[4 + j] & 0xFF) << (8 * j);
-              }
-              *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + m * N + 8 * word) =
-                  v2i{(int)lo4, (int)hi4};
+              lo4[q] |= (uint32_t)(c0 & 0xFF) << (8 * r);
+              hi4[q] |= (uint32_t)(c1 & 0xFF) << (8 * r);
             }
           }
+          *reinterpret_cast<v4i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + (16 * mb + li) * N +
+                                  8 * (8 * c + 2 * lg)) = v4i{(int)lo4[0], (int)hi4[0], (int)lo4[1], (int)hi4[1]};
+        }
       }
     }
   }
@@ -1246,9 +1324,10 @@ template <class DT, int MB, bool PACK>
 static int launch_duo(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right, float clip,
                       void* out_codes, float* out_scales, hipStream_t stream) {
   using T = typename DT::T;
-  // two workgroups (four waves, one per SIMD) per CU
-  const int64_t grid = std::min<int64_t>(tokens, (int64_t)device_cu_count() * 2);
-  hipLaunchKernelGGL((fq_duo_kernel<DT, MB, PACK>), dim3((unsigned)grid), dim3(128), 0, stream,
+  constexpr int SLOTS = DuoShape<MB>::SLOTS;
+  // one workgroup (four waves, one per SIMD) per CU
+  const int64_t grid = std::min<int64_t>((tokens + SLOTS - 1) / SLOTS, (int64_t)device_cu_count());
+  hipLaunchKernelGGL((fq_duo_kernel<DT, MB, PACK>), dim3((unsigned)grid), dim3(128 * SLOTS), 0, stream,
                      reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
                      reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
   return QO_OK;
