@@ -221,8 +221,8 @@ def cpu_baseline_gemm(torch, budget_s=8.0):
 
 # Kernel of each benched workload, as rocprofv3 names it (a substring of the demangled name).
 KERNEL_OF = {
-    "quantize_cfg2": "fq_mfma_kernel<qo::F16T, 4, 2, true>",
-    "quantize_cfg3": "fq_mfma_kernel<qo::BF16T, 7, 4, true>",
+    "quantize_cfg2": "fq_wave_kernel<qo::F16T, 4, 2, true>",
+    "quantize_cfg3": "fq_duo_kernel<qo::BF16T, 7, true>",
     "gemm_cfg4": "gemm_i4_dma<256, 224, 4, 2, 4, false, qo::OutF16>",
 }
 COPY_PROBE_BYTES = 1 << 30      # float32 negation of 1 GiB: reads and writes exactly this many bytes
@@ -436,6 +436,7 @@ def main():
              f"{secondary['gemm_cfg4']['TOPS']:.0f} TOPS")
         _log("secondary: config 3 quantize")
         secondary["quantize_cfg3"] = bench_quant(torch, wl.quant_cfg3(), args.steps, args.warmup, dev)
+        secondary["quantize_cfg3"]["roofline"]["traffic"] = _traffic_from_profiles("quantize_cfg3")
         _log(f"config 3: {secondary['quantize_cfg3']['us_per_step']:.1f} us/step, "
              f"{secondary['quantize_cfg3']['GBps']:.0f} GB/s")
         for t in (16, 4096):
