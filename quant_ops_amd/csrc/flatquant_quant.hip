@@ -805,6 +805,13 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
     la[0] = *reinterpret_cast<const V*>(base);
     la[1] = *reinterpret_cast<const V*>(base + 16 * M);
   }
+  // Waves issue their first token's loads about 320 cycles apart, in wave
+  // order: the memory system then returns a workgroup's tokens one after
+  // another instead of all of them at the end of the stream, so early tokens
+  // compute while later ones are still arriving (4-6% at 2048-8192 tokens of
+  // 64 x 64). The delay sits in a branch without memory instructions, which
+  // leaves the compiler's wait counts exact.
+  for (int k = 0; k < wave; ++k) __builtin_amdgcn_s_sleep(5);
   V xf[MB][KS1];
   fq_wave_load_x<DT, MB, NQ>(x + min(t, tokens - 1) * x_ld, xf, li, lg);
 
@@ -1015,17 +1022,6 @@ struct DuoShape {
   static_assert(XF % 2 == 0, "X fragments split over the pair");
 };
 
-// s_waitcnt vmcnt(n) for a wave-uniform runtime n: the largest of a few fixed
-// levels not above n (a smaller count is a stricter wait).
-template <int A, int B, int C>
-__device__ inline void wait_vmcnt_at_most(int n) {
-  static_assert(A < B && B < C, "levels ascending");
-  if (n >= C) wait_vmcnt<C>();
-  else if (n >= B) wait_vmcnt<B>();
-  else if (n >= A) wait_vmcnt<A>();
-  else wait_vmcnt<0>();
-}
-
 template <class DT, int MB, bool PACK>
 __global__ void __launch_bounds__(128 * DuoShape<MB>::SLOTS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
@@ -1120,20 +1116,15 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
 #pragma unroll
   for (int b = 0; b < XB; ++b) issue_x(t0 + b * step, b);
 
-  // Stores this wave issued in the last XB iterations (the output stores sit
-  // between the copies the next waits target, so the wait counts them).
-  constexpr int STORES = MB;   // output stores per wave and valid token (+1 scale store for c == 0)
-  int st_prev[XB] = {};
   for (int64_t it = 0; t0 - p + it * step < tokens; ++it) {
     const int64_t t = t0 + it * step;
     const int b = XB == 2 ? (int)(it & 1) : 0;
     unsigned char* const xb = xslot + b * S::X_BYTES;
-    // this iteration's copy is older than: the stores of the last XB
-    // iterations and the copies issued in the last XB - 1
-    int newer = (XB - 1) * (S::XF / 2);
-#pragma unroll
-    for (int k = 0; k < XB; ++k) newer += st_prev[k];
-    wait_vmcnt_at_most<S::XF / 2, S::XF / 2 + STORES, S::XF / 2 + 2 * STORES>(newer);
+    // This iteration's copy is older than the copies issued in the last
+    // XB - 1 iterations. The output stores issued in between are not counted:
+    // a store may complete out of order with the copies, and counting it
+    // could end the wait before this copy landed.
+    wait_vmcnt<(XB - 1) * (S::XF / 2)>();
     lds_barrier();   // the slot's X (and, the first time, the L fragments) visible
 
     // First product Z = X R for this wave's 64 columns, rounding point 1, the
@@ -1201,12 +1192,7 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     amax = DT::round(fmaxf(red[p][0], red[p][1]));
     const float s = fq_scale_abs<DT>(amax, clip);
 
-#pragma unroll
-    for (int k = XB - 1; k > 0; --k) st_prev[k] = st_prev[k - 1];
-    st_prev[0] = 0;
     if (t < tokens) {
-      // exactly STORES output stores (one per 16-row block), plus the scale
-      st_prev[0] = STORES + (c == 0 ? 1 : 0);
       if (c == 0 && lane == 0) out_scales[t] = s;
       const float rcp = 1.0f / s;
       if (PACK) {
