@@ -14,10 +14,11 @@ the wide quantize (config 3) and the end-to-end W4A4 linear (config 5).
 ``cpu_baseline`` times this repo's CPU restatement of the reference PyTorch
 fallback on a bounded sample on the host cores (a reported baseline, not a target).
 
-Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-secondary] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--warm-s 0.2] [--no-secondary] [--no-cpu]
        python bench.py --pmc-pass                       (under rocprofv3 --pmc FETCH_SIZE or WRITE_SIZE)
        python bench.py --pmc-summary FETCH_DIR WRITE_DIR
-       python bench.py --trace-summary KERNEL_TRACE_CSV    (rocprofv3 --kernel-trace --output-format csv)
+       python bench.py --trace-summary KERNEL_TRACE_CSV [--trace-last K]
+                                                        (rocprofv3 --kernel-trace --output-format csv)
 """
 import argparse
 import json
@@ -41,6 +42,9 @@ def _nbuf(bytes_per_set, minimum=2):
     return max(minimum, math.ceil(1.25 * MALL_BYTES / max(1, bytes_per_set)))
 
 
+WARM_S = 0.2   # minimum untimed warm-up per measurement
+
+
 def _time_graph(torch, launch, steps, warmup):
     """Warm up, capture ``steps`` launches in one graph, replay it once timed.
 
@@ -62,8 +66,16 @@ def _time_graph(torch, launch, steps, warmup):
             for i in range(steps):
                 launch(i)
     torch.cuda.synchronize()
-    g_warm.replay()
-    torch.cuda.synchronize()
+    # Replay the warm-up graph for at least WARM_S seconds (untimed): a GPU
+    # that has been idle runs its first fraction of a millisecond of short
+    # kernels measurably slower (clocks ramping), which would otherwise land
+    # in the timed replay of a small step.
+    deadline = time.perf_counter() + WARM_S
+    while True:
+        g_warm.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() >= deadline:
+            break
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     cur = torch.cuda.current_stream()
@@ -326,12 +338,14 @@ BENCH_SEGMENTS = [
 ]
 
 
-def trace_summary(trace_csv):
+def trace_summary(trace_csv, tail=None):
     """Per-workload kernel durations from a rocprofv3 --kernel-trace CSV of a default bench run.
 
     Dispatches of this library's kernels are split into segments (a new segment
     starts when a kernel reappears after more than 16 other dispatches) and the
-    segments, in dispatch order, are matched to BENCH_SEGMENTS.
+    segments, in dispatch order, are matched to BENCH_SEGMENTS. With ``tail``,
+    only the last ``tail`` dispatches of each segment count (the timed steps;
+    the warm-up replays come first).
     """
     import csv
     import statistics
@@ -354,7 +368,7 @@ def trace_summary(trace_csv):
     lines = [f"{'workload':22s} {'calls':>5s} {'avg_us':>9s} {'median_us':>9s} {'min_us':>9s} {'max_us':>9s} "
              f"{'GB/s':>7s} {'TOP/s':>7s}  kernel [grid x block]"]
     for i, s in enumerate(segs):
-        d = s["dur"]
+        d = s["dur"][-tail:] if tail else s["dur"]
         avg = sum(d) / len(d) / 1e3
         name, nbytes, ops = BENCH_SEGMENTS[i] if labelled else (f"segment {i}", None, None)
         gbs = f"{nbytes / avg / 1e3:7.0f}" if nbytes else f"{'':7s}"
@@ -378,16 +392,21 @@ def _traffic_from_profiles(kernel_key):
 
 
 def main():
+    global WARM_S
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warm-s", type=float, default=WARM_S,
+                    help="minimum seconds of untimed warm-up replays per measurement (default %(default)s)")
     ap.add_argument("--no-secondary", action="store_true", help="only the primary workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="eager launches of each benched kernel and a copy probe, for rocprofv3 --pmc")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="per-workload kernel durations from a rocprofv3 kernel trace of a default run")
+    ap.add_argument("--trace-last", type=int, default=None, metavar="K",
+                    help="with --trace-summary: only the last K dispatches of each workload (the timed steps)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print per-launch HBM bytes from two rocprofv3 --pmc output folders")
     args = ap.parse_args()
@@ -395,15 +414,16 @@ def main():
         pmc_summary(*args.pmc_summary)
         return
     if args.trace_summary:
-        trace_summary(args.trace_summary)
+        trace_summary(args.trace_summary, args.trace_last)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the hot path shards over tokens with no "
               f"communication); --gpus {args.gpus} is not supported", file=sys.stderr)
         sys.exit(2)
-    if args.steps < 1 or args.warmup < 0:
-        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+    if args.steps < 1 or args.warmup < 0 or args.warm_s < 0:
+        print("bench.py: --steps must be >= 1, --warmup and --warm-s >= 0", file=sys.stderr)
         sys.exit(2)
+    WARM_S = args.warm_s
 
     import torch
 
