@@ -181,6 +181,48 @@ def bench_linear(torch, tokens, steps, warmup, dev):
             "weight_GBps": 4096 * 1792 * 4 / per_step_s / 1e9, "note": "quantize + GEMM, L2/MALL-warm inputs"}
 
 
+LAYOUT_ROWS, LAYOUT_K = 14336, 4096   # the config 4 weight W [N, K] as int8 codes
+
+
+def bench_layout(torch, steps, warmup, dev):
+    """Weight-prep kernels at the config 4 weight: pack int8 codes [14336, 4096] ->
+    int32 [14336, 512], unpack it back, and transpose the packed words to the
+    [K/8, N] = [512, 14336] layout. HBM-bound; bytes are input + output."""
+    from quant_ops_amd import capi
+
+    g = torch.Generator().manual_seed(51)
+    codes0 = torch.randint(-8, 8, (LAYOUT_ROWS, LAYOUT_K), generator=g, dtype=torch.int8).to(dev)
+    words0 = capi.pack_int4_to_int32(codes0)
+    res = {}
+    cases = (
+        ("pack", codes0, lambda src, dst: capi.pack_int4_to_int32(src, out=dst), (LAYOUT_ROWS, LAYOUT_K // 8),
+         torch.int32),
+        ("unpack", words0, lambda src, dst: capi.unpack_int32_to_int4(src, out=dst), (LAYOUT_ROWS, LAYOUT_K),
+         torch.int8),
+        ("transpose", words0, lambda src, dst: capi.transpose_int32(src, out=dst), (LAYOUT_K // 8, LAYOUT_ROWS),
+         torch.int32),
+    )
+    for name, src0, fn, out_shape, out_dtype in cases:
+        nbytes = src0.numel() * src0.element_size() + math.prod(out_shape) * torch.empty((), dtype=out_dtype).element_size()
+        nbuf = _nbuf(nbytes)
+        srcs = [src0] + [src0.clone() for _ in range(nbuf - 1)]
+        dsts = [torch.empty(out_shape, dtype=out_dtype, device=dev) for _ in range(nbuf)]
+
+        def launch(i, fn=fn, srcs=srcs, dsts=dsts, nbuf=nbuf):
+            fn(srcs[i % nbuf], dsts[i % nbuf])
+
+        gpu_ms, _ = _time_graph(torch, launch, steps, warmup)
+        per_step_s = gpu_ms / 1e3 / steps
+        gbs = nbytes / per_step_s / 1e9
+        res[name] = {"bytes_per_step": nbytes, "us_per_step": per_step_s * 1e6, "GBps": gbs, "buffers_rotated": nbuf,
+                     "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": gbs / HBM_PEAK_GBS}}
+        del srcs, dsts
+    del codes0, words0
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(torch, budget_s=12.0):
     """The oracle (CPU restatement of the reference fallback) on config 2, bounded in time."""
     from oracle import fq_reference as ofq
@@ -335,6 +377,9 @@ BENCH_SEGMENTS = [
     ("cfg5 T=16 gemm", None, 2 * 16 * 4096 * 14336),
     ("cfg5 T=4096 quantize", 4096 * 14336 * 2 + 4096 * 1792 * 4 + 4096 * 4 + 2 * (112 * 112 + 128 * 128), None),
     ("cfg5 T=4096 gemm", None, 2 * 4096 * 4096 * 14336),
+    ("pack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
+    ("unpack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
+    ("transpose cfg4 weight", 2 * 14336 * 512 * 4, None),
 ]
 
 
@@ -462,6 +507,8 @@ def main():
         for t in (16, 4096):
             _log(f"secondary: config 5 linear T={t}")
             secondary[f"linear_cfg5_T{t}"] = bench_linear(torch, t, args.steps, args.warmup, dev)
+        _log("secondary: weight layout kernels (config 4 weight)")
+        secondary["layout_cfg4_weight"] = bench_layout(torch, args.steps, args.warmup, dev)
 
     cpu = None
     if not args.no_cpu:

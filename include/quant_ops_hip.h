@@ -118,6 +118,49 @@ int qo_int4_gemm(const int32_t* a, int64_t lda,
 int qo_dequantize_int4(const void* codes, int pack_int32, const void* scales, int scale_dtype,
                        int64_t tokens, int64_t features, float* out, void* stream);
 
+/*
+ * Pack int8 codes into int32 words: word p of a row =
+ * sum_i ((codes[8p + i] + 8) mod 256) << 4i (mod 2^32), i.e. code + 8 in
+ * nibble i for codes in [-8, 7]; other int8 values wrap exactly as the
+ * reference's int8 add / uint8 cast / int32 sum do.
+ *
+ * Replaces pack_int4_to_int32 (int4_matmul/ops.py:23-45) and the activation /
+ * weight packing of pack_int4_to_int32_manual
+ * (w4a4_flatquant_dynamic.py:43-67, after its clamp).
+ *
+ *   codes   int8 [rows, features], row stride codes_ld (elements)
+ *   out     int32 [rows, features / 8], row stride out_ld; features % 8 == 0
+ */
+int qo_pack_int4_to_int32(const int8_t* codes, int64_t codes_ld, int64_t rows, int64_t features,
+                          int32_t* out, int64_t out_ld, void* stream);
+
+/*
+ * Unpack int32 words into int8 codes: out[8p + i] = ((word_p >> 4i) & 0xF) - 8.
+ *
+ * Replaces unpack_int32_to_int4 (int4_matmul/ops.py:48-66).
+ *
+ *   words   int32 [rows, nwords], row stride words_ld (elements)
+ *   out     int8 [rows, 8 * nwords], row stride out_ld
+ */
+int qo_unpack_int32_to_int4(const int32_t* words, int64_t words_ld, int64_t rows, int64_t nwords,
+                            int8_t* out, int64_t out_ld, void* stream);
+
+/*
+ * Transpose a matrix of 32-bit words: out[c, r] = in[r, c].
+ *
+ * Converts a packed int4 weight between the GEMM's two B layouts, [K/8, N]
+ * (word [p, n] holds k = 8p .. 8p+7 of column n) and [N, K/8] (row-major
+ * W packed along K), which hold the same words. Replaces the
+ * pack(b.T).T / .t().contiguous() round trips of
+ * examples/int4_matmul_benchmark.py:21-22 and
+ * w4a4_flatquant_dynamic.py:290-292.
+ *
+ *   in      int32 [rows, cols], row stride in_ld
+ *   out     int32 [cols, rows], row stride out_ld
+ */
+int qo_transpose_int32(const int32_t* in, int64_t in_ld, int64_t rows, int64_t cols, int32_t* out,
+                       int64_t out_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

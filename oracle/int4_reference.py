@@ -16,15 +16,18 @@ import torch
 
 
 def pack_int4_to_int32(codes) -> np.ndarray:
-    """Pack int codes in [-8, 7] of shape [rows, F] (F % 8 == 0) to int32 [rows, F/8].
+    """Pack int8 codes of shape [rows, F] (F % 8 == 0) to int32 [rows, F/8].
 
-    Reference: ``int4_matmul/ops.py:23-45``.
+    Reference: ``int4_matmul/ops.py:23-45``: ``(tensor + 8).to(torch.uint8)``
+    keeps the low 8 bits of code + 8 (the int8 add wraps, the cast takes the
+    value mod 256), and the shifted int32 sum wraps mod 2^32. For codes in
+    [-8, 7] that is code + 8 in nibble i of the word.
     """
     q = np.asarray(codes).astype(np.int64)
     rows, feats = q.shape
     if feats % 8:
         raise ValueError(f"features ({feats}) must be divisible by 8")
-    u = (q + 8).astype(np.uint64).reshape(rows, feats // 8, 8)
+    u = ((q + 8) & 0xFF).astype(np.uint64).reshape(rows, feats // 8, 8)
     shifts = (np.arange(8, dtype=np.uint64) * np.uint64(4))
     word = (u << shifts).sum(axis=2) & np.uint64(0xFFFFFFFF)
     return word.astype(np.uint32).view(np.int32)

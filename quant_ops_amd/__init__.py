@@ -25,8 +25,10 @@ from .int4_matmul import (
     int4_matmul_cuda,
     int4_matmul_pytorch,
     pack_int4_to_int32,
+    transpose_packed,
     unpack_int32_to_int4,
 )
+from .linear import prepare_w4a4_weight, w4a4_flatquant_linear
 from .decompose import get_decompose_dim
 from . import meta_ops  # noqa: F401  (registers fakes once the schemas exist)
 

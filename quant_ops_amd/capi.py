@@ -19,7 +19,8 @@ STATUS = {0: "QO_OK", 1: "QO_ERR_NULL_POINTER", 2: "QO_ERR_SHAPE", 3: "QO_ERR_DT
 
 # Every symbol the header declares; the CPU tests check they are all exported.
 EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_flatquant_quantize",
-            "qo_int4_gemm", "qo_dequantize_int4")
+            "qo_int4_gemm", "qo_dequantize_int4", "qo_pack_int4_to_int32", "qo_unpack_int32_to_int4",
+            "qo_transpose_int32")
 
 _TORCH_CODE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
@@ -56,6 +57,10 @@ def lib():
                                c_i64, c_i64, c_i64, c_vp]
     L.qo_dequantize_int4.restype = c_int
     L.qo_dequantize_int4.argtypes = [c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_vp, c_vp]
+    for name in ("qo_pack_int4_to_int32", "qo_unpack_int32_to_int4", "qo_transpose_int32"):
+        fn = getattr(L, name)
+        fn.restype = c_int
+        fn.argtypes = [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp]
     _lib = L
     return L
 
@@ -134,4 +139,41 @@ def dequantize_int4(codes, scales, packed_int32=False, out=None, stream=None):
         ctypes.c_void_p(codes.data_ptr()), 1 if packed_int32 else 0,
         ctypes.c_void_p(scales.data_ptr()), _TORCH_CODE[scales.dtype], t, f,
         ctypes.c_void_p(out.data_ptr()), _stream(stream)))
+    return out
+
+
+def _ld(t):
+    return t.stride(0) if t.dim() == 2 and t.shape[0] > 1 else t.shape[-1]
+
+
+def pack_int4_to_int32(codes, out=None, stream=None):
+    """Call ``qo_pack_int4_to_int32``: int8 [rows, F] -> int32 [rows, F/8] (rows may be strided)."""
+    assert codes.dtype == torch.int8 and codes.dim() == 2 and codes.stride(1) == 1
+    rows, feats = codes.shape
+    if out is None:
+        out = torch.empty((rows, feats // 8), dtype=torch.int32, device=codes.device)
+    _check(lib().qo_pack_int4_to_int32(ctypes.c_void_p(codes.data_ptr()), _ld(codes), rows, feats,
+                                       ctypes.c_void_p(out.data_ptr()), _ld(out), _stream(stream)))
+    return out
+
+
+def unpack_int32_to_int4(words, out=None, stream=None):
+    """Call ``qo_unpack_int32_to_int4``: int32 [rows, W] -> int8 [rows, 8W] (rows may be strided)."""
+    assert words.dtype == torch.int32 and words.dim() == 2 and words.stride(1) == 1
+    rows, nw = words.shape
+    if out is None:
+        out = torch.empty((rows, 8 * nw), dtype=torch.int8, device=words.device)
+    _check(lib().qo_unpack_int32_to_int4(ctypes.c_void_p(words.data_ptr()), _ld(words), rows, nw,
+                                         ctypes.c_void_p(out.data_ptr()), _ld(out), _stream(stream)))
+    return out
+
+
+def transpose_int32(x, out=None, stream=None):
+    """Call ``qo_transpose_int32``: int32 [R, C] -> contiguous int32 [C, R]."""
+    assert x.dtype == torch.int32 and x.dim() == 2 and x.stride(1) == 1
+    rows, cols = x.shape
+    if out is None:
+        out = torch.empty((cols, rows), dtype=torch.int32, device=x.device)
+    _check(lib().qo_transpose_int32(ctypes.c_void_p(x.data_ptr()), _ld(x), rows, cols,
+                                    ctypes.c_void_p(out.data_ptr()), _ld(out), _stream(stream)))
     return out

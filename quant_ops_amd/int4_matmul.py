@@ -22,19 +22,51 @@ def _shifts(device):
 
 
 def pack_int4_to_int32(tensor: torch.Tensor) -> torch.Tensor:
-    """int8 codes in [-8, 7] [rows, F] -> int32 [rows, F/8] (``int4_matmul/ops.py:23-45``)."""
+    """int8 codes in [-8, 7] [rows, F] -> int32 [rows, F/8] (``int4_matmul/ops.py:23-45``).
+
+    GPU int8 tensors use the HIP kernel ``qo_pack_int4_to_int32``; other inputs
+    run the reference's torch formula.
+    """
     rows, feats = tensor.shape
     assert feats % 8 == 0, f"features ({feats}) must be divisible by 8"
+    if tensor.is_cuda and tensor.dtype == torch.int8:
+        _loader.require_kernels("pack_int4_to_int32")
+        from . import capi
+        return capi.pack_int4_to_int32(tensor if tensor.stride(1) == 1 else tensor.contiguous())
     nib = (tensor + 8).to(torch.uint8).view(rows, feats // 8, 8).to(torch.int32)
     words = (nib << _shifts(tensor.device)).sum(dim=2, dtype=torch.int64)
     return torch.where(words >= 2**31, words - 2**32, words).to(torch.int32)
 
 
 def unpack_int32_to_int4(packed: torch.Tensor) -> torch.Tensor:
-    """int32 [rows, W] -> int8 codes [rows, 8W] (``int4_matmul/ops.py:48-66``)."""
+    """int32 [rows, W] -> int8 codes [rows, 8W] (``int4_matmul/ops.py:48-66``).
+
+    GPU int32 tensors use the HIP kernel ``qo_unpack_int32_to_int4``.
+    """
+    if packed.is_cuda and packed.dtype == torch.int32:
+        _loader.require_kernels("unpack_int32_to_int4")
+        from . import capi
+        return capi.unpack_int32_to_int4(packed if packed.stride(1) == 1 else packed.contiguous())
     rows, words = packed.shape
     nib = (packed.unsqueeze(-1) >> _shifts(packed.device)) & 0xF
     return (nib - 8).to(torch.int8).reshape(rows, words * 8)
+
+
+def transpose_packed(packed: torch.Tensor) -> torch.Tensor:
+    """Contiguous transpose of a packed int32 matrix: converts a weight between
+    the GEMM's B layouts [K/8, N] and [N, K/8], which hold the same words.
+
+    The reference spells this ``.t().contiguous()`` / ``pack(b.T).T``
+    (``examples/int4_matmul_benchmark.py:21-22``,
+    ``w4a4_flatquant_dynamic.py:290-292``). GPU tensors use the HIP kernel
+    ``qo_transpose_int32``.
+    """
+    assert packed.dtype == torch.int32 and packed.dim() == 2, "int32 [rows, cols] expected"
+    if packed.is_cuda:
+        _loader.require_kernels("transpose_packed")
+        from . import capi
+        return capi.transpose_int32(packed if packed.stride(1) == 1 else packed.contiguous())
+    return packed.t().contiguous()
 
 
 def int4_matmul_pytorch(

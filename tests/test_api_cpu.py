@@ -10,6 +10,7 @@ import torch
 
 import quant_ops_amd as qo
 from quant_ops_amd import _loader, capi
+from quant_ops_amd import workloads as wl
 from oracle import fq_reference as ofq
 from oracle import int4_reference as oi4
 
@@ -110,6 +111,53 @@ def test_pack_unpack_match_oracle():
     w = qo.pack_int4_to_int32(q)
     assert np.array_equal(w.numpy(), oi4.pack_int4_to_int32(q.numpy()))
     assert torch.equal(qo.unpack_int32_to_int4(w), q)
+
+
+def test_transpose_packed_cpu():
+    w = torch.arange(6 * 10, dtype=torch.int32).view(6, 10)
+    t = qo.transpose_packed(w)
+    assert t.is_contiguous() and torch.equal(t, w.t())
+    # a [K/8, N] weight built as pack(b.T).T and the [N, K/8] packing of the same
+    # codes are transposes of each other
+    g = torch.Generator().manual_seed(8)
+    codes = torch.randint(-8, 8, (12, 32), generator=g, dtype=torch.int8)   # [N, K]
+    assert torch.equal(qo.transpose_packed(qo.pack_int4_to_int32(codes)),
+                       qo.pack_int4_to_int32(codes).t().contiguous())
+
+
+def test_prepare_weight_clamps_then_packs():
+    w = torch.tensor([[-20, -8, -1, 0, 3, 7, 8, 100]], dtype=torch.int32)
+    packed = qo.prepare_w4a4_weight(w)
+    # clamp to [-8, 7] first (pack_int4_to_int32_manual): codes -8 -8 -1 0 3 7 7 7
+    expect = sum((c + 8) << (4 * i) for i, c in enumerate([-8, -8, -1, 0, 3, 7, 7, 7]))
+    assert packed.dtype == torch.int32 and int(packed[0, 0]) & 0xFFFFFFFF == expect
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_w4a4_linear_cpu_composes_quantize_and_gemm(dtype):
+    """The linear equals quantize -> int4 GEMM on W.t() -> + bias, and, with
+    orthogonal transforms, approximates x @ W_deqᵀ (a transposed weight or a
+    transform applied on the wrong side fails the second check)."""
+    g = torch.Generator().manual_seed(12)
+    m, n, out_f, t = 4, 8, 16, 6
+    x = torch.randn(2, t // 2, m * n, generator=g).to(dtype)
+    L, R = wl.orthogonal(m, 31).to(dtype), wl.orthogonal(n, 32).to(dtype)
+    wc = torch.randint(-8, 8, (out_f, m * n), generator=g, dtype=torch.int8)
+    sw = (torch.rand(out_f, generator=g) * 0.1 + 0.01).float()
+    bias = torch.randn(out_f, generator=g).to(dtype)
+    wp = qo.prepare_w4a4_weight(wc)
+    y = qo.w4a4_flatquant_linear(x, L, R, wp, sw.view(-1, 1), clip_ratio=1.0, bias=bias)
+    assert y.shape == (2, t // 2, out_f) and y.dtype == dtype
+    q, s = ofq.flatquant_pytorch(x.reshape(-1, m * n), L, R, 1.0, True)
+    ref = oi4.int4_matmul_pytorch(q, wp.t(), s.float(), sw, out_dtype=dtype) + bias
+    assert torch.equal(y.reshape(-1, out_f), ref)
+    # Y = quantized (x·kron(L,R)); W acts on the transformed input, so compare
+    # with (x·kron(L,R)) @ (W·diag)ᵀ in float64
+    kron = torch.kron(L.double(), R.double())
+    xt = x.reshape(-1, m * n).double() @ kron
+    exact = xt @ (wc.double() * sw.double().view(-1, 1)).t() + bias.double()
+    rel = (y.reshape(-1, out_f).double() - exact).norm() / exact.norm()
+    assert rel < 0.15
 
 
 def test_int4_matmul_cpu_matches_oracle():

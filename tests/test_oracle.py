@@ -53,6 +53,20 @@ def test_pack_known_answers():
     assert oi4.pack_int4_to_int32(np.zeros((1, 8), np.int8))[0, 0] == np.int32(np.uint32(0x88888888).view(np.int32))
 
 
+def test_pack_known_answers_out_of_range_codes():
+    # (q + 8) mod 256 per code, shifted sums mod 2^32 (int8 add, uint8 cast and
+    # int32 sum of int4_matmul/ops.py:36-43), worked by hand:
+    #   127 -> 0x87: 0x87 * 0x11111111 = 0x8FFFFFFF7 -> 0xFFFFFFF7
+    #  -128 -> 0x88: 0x88 * 0x11111111 = 0x911111108 -> 0x11111108
+    #   -9  -> 0xFF in slot 0 only: 0xFF + 0x88888880 (the seven zero codes)
+    def word(codes):
+        return int(np.uint32(oi4.pack_int4_to_int32(np.array([codes], dtype=np.int8))[0, 0].view(np.uint32)))
+
+    assert word([127] * 8) == 0xFFFFFFF7
+    assert word([-128] * 8) == 0x11111108
+    assert word([-9] + [0] * 7) == 0x8888897F
+
+
 def test_pack_closed_form_and_roundtrip():
     rng = np.random.default_rng(0)
     q = rng.integers(-8, 8, size=(17, 64), dtype=np.int8)
