@@ -17,6 +17,7 @@ fallback on a bounded sample on the host cores (a reported baseline, not a targe
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--warm-s 0.2] [--no-secondary] [--no-cpu]
        python bench.py --pmc-pass                       (under rocprofv3 --pmc FETCH_SIZE or WRITE_SIZE)
        python bench.py --pmc-summary FETCH_DIR WRITE_DIR
+       python bench.py --pmc-table PMC_DIR [PMC_DIR ...]
        python bench.py --trace-summary KERNEL_TRACE_CSV [--trace-last K]
                                                         (rocprofv3 --kernel-trace --output-format csv)
 """
@@ -320,6 +321,35 @@ def pmc_pass(torch, dev):
     print(json.dumps({"pmc_pass": True, "copy_probe_bytes": COPY_PROBE_BYTES, "kernels": KERNEL_OF}), flush=True)
 
 
+def pmc_table(dirs):
+    """Counter table of the benched kernels from rocprofv3 --pmc runs of --pmc-pass.
+
+    For every counter found in the counter_collection CSVs under ``dirs``: the
+    value per dispatch (rows of one dispatch summed), median over the dispatches
+    of each kernel in KERNEL_OF.
+    """
+    import csv
+    import glob
+    import statistics
+
+    vals = {}
+    for root in dirs:
+        for path in glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True):
+            with open(path, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    key = (row["Counter_Name"], row["Kernel_Name"], row["Dispatch_Id"])
+                    vals[key] = vals.get(key, 0.0) + float(row["Counter_Value"])
+    counters = sorted({c for c, _, _ in vals})
+    names = list(KERNEL_OF)
+    print(f"{'counter':34s} " + " ".join(f"{n:>14s}" for n in names))
+    for c in counters:
+        cells = []
+        for n in names:
+            hits = [v for (cc, kn, _), v in vals.items() if cc == c and KERNEL_OF[n] in kn]
+            cells.append(f"{statistics.median(hits):14.4g}" if hits else f"{'-':>14s}")
+        print(f"{c:34s} " + " ".join(cells))
+
+
 def pmc_summary(fetch_dir, write_dir):
     """Per-launch HBM bytes of each benched kernel from two rocprofv3 --pmc runs.
 
@@ -454,9 +484,14 @@ def main():
                     help="with --trace-summary: only the last K dispatches of each workload (the timed steps)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print per-launch HBM bytes from two rocprofv3 --pmc output folders")
+    ap.add_argument("--pmc-table", nargs="+", metavar="PMC_DIR",
+                    help="per-kernel medians of every counter in rocprofv3 --pmc output folders of --pmc-pass")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.pmc_table:
+        pmc_table(args.pmc_table)
         return
     if args.trace_summary:
         trace_summary(args.trace_summary, args.trace_last)

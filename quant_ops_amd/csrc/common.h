@@ -140,6 +140,14 @@ __device__ inline uint32_t lds_addr(P* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
 
+// Workgroup barriers without the release/acquire fences of __syncthreads():
+// those fences wait for every outstanding vector-memory operation (vmcnt(0)),
+// which would also wait for loads still in flight for later stages or tokens.
+// The "memory" clobber keeps the compiler from moving memory accesses across
+// the barrier; lds_barrier first waits for this wave's LDS accesses.
+__device__ inline void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 }  // namespace qo
 
 // Thread-local error message used by qo_last_error().

@@ -375,13 +375,6 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Workgroup barriers without the release/acquire fences of __syncthreads():
-// those fences wait for every outstanding vector-memory operation (vmcnt(0)),
-// which would also wait for the next group's X prefetch. The "memory" clobber
-// keeps the compiler from moving memory accesses across the barrier.
-__device__ inline void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
-__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // One token group (this wave's token slot and pair) from an X stage in LDS:
 // both products, the per-token scale and the codes.
 template <class DT, int MB, int NP, bool PACK>
