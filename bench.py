@@ -182,6 +182,35 @@ def bench_linear(torch, tokens, steps, warmup, dev):
             "weight_GBps": 4096 * 1792 * 4 / per_step_s / 1e9, "note": "quantize + GEMM, L2/MALL-warm inputs"}
 
 
+def bench_dequant(torch, steps, warmup, dev):
+    """dequantize_int4 of config 2's output: packed int32 [2048, 512] codes + fp32
+    scales -> fp32 [2048, 4096]. HBM-bound: 4 B of codes and 32 B of float32 per
+    8 features, plus the scales."""
+    from quant_ops_amd import capi
+
+    t, f = 2048, 4096
+    g = torch.Generator().manual_seed(52)
+    codes0 = torch.randint(-2**31, 2**31, (t, f // 8), generator=g, dtype=torch.int64).to(torch.int32).to(dev)
+    scales0 = torch.rand(t, generator=g).to(dev)
+    nbytes = t * f // 2 + t * 4 + t * f * 4
+    nbuf = _nbuf(nbytes)
+    codes = [codes0] + [codes0.clone() for _ in range(nbuf - 1)]
+    outs = [torch.empty(t, f, dtype=torch.float32, device=dev) for _ in range(nbuf)]
+
+    def launch(i):
+        capi.dequantize_int4(codes[i % nbuf], scales0, True, out=outs[i % nbuf])
+
+    gpu_ms, _ = _time_graph(torch, launch, steps, warmup)
+    per_step_s = gpu_ms / 1e3 / steps
+    gbs = nbytes / per_step_s / 1e9
+    del codes, outs
+    torch.cuda.empty_cache()
+    return {"workload": "dequantize_int4 packed [2048, 512] -> fp32 [2048, 4096]", "bytes_per_step": nbytes,
+            "us_per_step": per_step_s * 1e6, "GBps": gbs, "buffers_rotated": nbuf,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS}}
+
+
 LAYOUT_ROWS, LAYOUT_K = 14336, 4096   # the config 4 weight W [N, K] as int8 codes
 
 
@@ -410,6 +439,7 @@ BENCH_SEGMENTS = [
     ("pack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
     ("unpack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
     ("transpose cfg4 weight", 2 * 14336 * 512 * 4, None),
+    ("dequantize cfg2 codes", 2048 * 4096 // 2 + 2048 * 4 + 2048 * 4096 * 4, None),
 ]
 
 
@@ -544,6 +574,8 @@ def main():
             secondary[f"linear_cfg5_T{t}"] = bench_linear(torch, t, args.steps, args.warmup, dev)
         _log("secondary: weight layout kernels (config 4 weight)")
         secondary["layout_cfg4_weight"] = bench_layout(torch, args.steps, args.warmup, dev)
+        _log("secondary: dequantize (config 2 codes)")
+        secondary["dequant_cfg2"] = bench_dequant(torch, args.steps, args.warmup, dev)
 
     cpu = None
     if not args.no_cpu:
