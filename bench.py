@@ -49,31 +49,28 @@ WARM_S = 0.2   # minimum untimed warm-up per measurement
 def _time_graph(torch, launch, steps, warmup):
     """Warm up, capture ``steps`` launches in one graph, replay it once timed.
 
-    Returns (gpu_ms_total, wall_s_total). ``launch(i)`` issues step i on the
-    current stream.
+    Warm-up: ``warmup`` eager launches, then untimed replays of the same graph
+    for at least WARM_S seconds. Replaying the timed graph itself touches every
+    rotated buffer in the timed order before the timed replay (a shorter
+    warm-up graph left the last buffers' first touch inside the timed
+    replay), and the time floor covers the clock ramp of a GPU that has been
+    idle. Returns (gpu_ms_total, wall_s_total) of the timed replay.
+    ``launch(i)`` issues step i on the current stream.
     """
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
-    g_warm = torch.cuda.CUDAGraph()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
-        with torch.cuda.graph(g_warm, stream=stream):
-            for i in range(max(1, warmup)):
-                launch(i)
         with torch.cuda.graph(g, stream=stream):
             for i in range(steps):
                 launch(i)
     torch.cuda.synchronize()
-    # Replay the warm-up graph for at least WARM_S seconds (untimed): a GPU
-    # that has been idle runs its first fraction of a millisecond of short
-    # kernels measurably slower (clocks ramping), which would otherwise land
-    # in the timed replay of a small step.
     deadline = time.perf_counter() + WARM_S
     while True:
-        g_warm.replay()
+        g.replay()
         torch.cuda.synchronize()
         if time.perf_counter() >= deadline:
             break
