@@ -1055,20 +1055,23 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     }
   };
 
-  // Set-up, once per workgroup. L and R are copied row-major into LDS by
-  // LDS-DMA (coalesced 16-byte chunks), then rearranged into fragments from
-  // LDS: R first (N*N elements) into this wave's registers, then L (over the
-  // X area) into the L fragments.
-  static_assert(M * M * 2 <= S::XAREA, "L staging space");
-  auto stage_rows = [&](const T* src, int chunks) {   // chunk c (8 elements) -> lds_all + 16 c
+  // Set-up, once per workgroup. R and L are copied row-major into the X area
+  // by LDS-DMA (coalesced 16-byte chunks; R at the start, L after it, one
+  // round trip for both), then rearranged from LDS: R into this wave's
+  // registers, L into the L fragments.
+  static_assert(N * N * 2 + M * M * 2 <= S::XAREA, "R and L staging space");
+  {
     const uint32_t lb = lds_addr(lds_all);
+    auto stage_rows = [&](const T* src, int chunks, uint32_t base) {   // chunk c (8 elements) -> base + 16 c
 #pragma unroll 1
-    for (int c0 = wave * 64; c0 < chunks; c0 += 64 * 2 * SLOTS)
-      if (c0 + lane < chunks) dma16(src + 8 * (c0 + lane), lb + 16 * c0);
+      for (int c0 = wave * 64; c0 < chunks; c0 += 64 * 2 * SLOTS)
+        if (c0 + lane < chunks) dma16(src + 8 * (c0 + lane), base + 16 * c0);
+    };
+    stage_rows(right, N * N / 8, lb);
+    stage_rows(left, M * M / 8, lb + N * N * 2);
     wait_vmcnt<0>();
     lds_barrier();
-  };
-  stage_rows(right, N * N / 8);
+  }
   // R fragments of this wave's columns: rf[q][h][ks][j] = R[32ks + 8lg + j][n],
   // n = 64c + 16(li/4) + 8q + 4h + li%4.
   V rf[2][2][KS1];
@@ -1085,13 +1088,11 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
           for (int j = 0; j < 8; ++j) rf[q][h][ks][j] = rs[(32 * ks + 8 * lg + j) * N + n];
       }
   }
-  lds_barrier();   // R is in registers; the staging space is free
-  stage_rows(left, M * M / 8);
   // L fragments (16 bytes per lane and slab): slab (mb, s), lane l, element j
   // holds L[32s + 16(j/4) + 4(l/16) + j%4][16mb + l%16]; in the zero-padded
   // tail slab (s = KS2, M / 16 odd) elements 4..7 are zero.
   {
-    const T* ls = reinterpret_cast<const T*>(lds_all);
+    const T* ls = reinterpret_cast<const T*>(lds_all + N * N * 2);
 #pragma unroll 1
     for (int fr = wave; fr < MB * S::KSL; fr += 2 * SLOTS) {
       const int mb = fr / S::KSL, sl = fr % S::KSL;
@@ -1105,7 +1106,7 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
       *reinterpret_cast<V*>(lfs + fr * 1024 + 16 * lane) = v;
     }
   }
-  lds_barrier();   // L fragments written, the X area is free
+  lds_barrier();   // R in registers, L fragments written: the X area is free
 #pragma unroll
   for (int b = 0; b < XB; ++b) issue_x(t0 + b * step, b);
 
