@@ -361,6 +361,59 @@ __device__ inline void with_scale_dtype(int code, F&& f) {
   else f(std::integral_constant<int, QO_DTYPE_BF16>{});
 }
 
+// Epilogue of a wave's FM x FN blocks of a tile: undo the 256x scale of the
+// widened operands, two float32 products (acc * sa) * sb, one rounding to the
+// output type. acc[i][j][r] holds C[m][n], m = mrow + 16i + li,
+// n = ncol + 16j + 4lg + r (the transposed product), so a lane stores four
+// adjacent outputs; rows and columns past the matrix edge are skipped.
+template <int FM, int FN, class OT>
+__device__ inline void store_c_blocks(const v4i (&acc)[FM][FN], const void* sa, int sad, const void* sb, int sbd,
+                                      typename OT::T* out, int64_t ldc, int M, int N, int mrow, int ncol, int li,
+                                      int lg) {
+  using T = typename OT::T;
+  float sav[FM], sbv[FN][4];
+  with_scale_dtype(sad, [&](auto dt) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) sav[i] = scale_at<decltype(dt)::value>(sa, min(mrow + 16 * i + li, M - 1));
+  });
+  with_scale_dtype(sbd, [&](auto dt) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sbv[j][r] = scale_at<decltype(dt)::value>(sb, min(ncol + 16 * j + 4 * lg + r, N - 1));
+  });
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = mrow + 16 * i + li;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = ncol + 16 * j + 4 * lg;
+      if (n >= N) continue;
+      T v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(acc[i][j][r] >> 8, sav[i], sbv[j][r]));
+      T* o = out + (int64_t)m * ldc + n;
+      if (n + 3 < N) {
+        if constexpr (sizeof(T) == 2) {
+          typedef short v4s __attribute__((ext_vector_type(4)));
+          v4s pk;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
+          *reinterpret_cast<v4s*>(o) = pk;
+        } else {
+          *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) o[r] = v[r];
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int WGM, int WGN, int STAGES, bool B_NK, class OT>
 __global__ void __launch_bounds__(64 * WGM * WGN, 1)
 gemm_i4_dma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
@@ -504,49 +557,7 @@ gemm_i4_dma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restric
   }
   gemm_wait_vmcnt<0>();
 
-  // Epilogue: undo the 256x scale, two float32 products, one rounding.
-  using T = typename OT::T;
-  float sav[FM], sbv[FN][4];
-  with_scale_dtype(sad, [&](auto dt) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) sav[i] = scale_at<decltype(dt)::value>(sa, min(m0 + wm * WM + 16 * i + li, M - 1));
-  });
-  with_scale_dtype(sbd, [&](auto dt) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sbv[j][r] = scale_at<decltype(dt)::value>(sb, min(n0 + wn * WN + 16 * j + 4 * lg + r, N - 1));
-  });
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * WM + 16 * i + li;
-    if (m >= M) continue;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * WN + 16 * j + 4 * lg;
-      if (n >= N) continue;
-      T v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(acc[i][j][r] >> 8, sav[i], sbv[j][r]));
-      T* o = out + (int64_t)m * ldc + n;
-      if (n + 3 < N) {
-        if constexpr (sizeof(T) == 2) {
-          typedef short v4s __attribute__((ext_vector_type(4)));
-          v4s pk;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
-          *reinterpret_cast<v4s*>(o) = pk;
-        } else {
-          *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n + r < N) o[r] = v[r];
-      }
-    }
-  }
+  store_c_blocks<FM, FN, OT>(acc, sa, sad, sb, sbd, out, ldc, M, N, m0 + wm * WM, n0 + wn * WN, li, lg);
 }
 
 // ---------------------------------------------------------------------------
@@ -708,48 +719,7 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
   }
   gemm_wait_vmcnt<0>();
 
-  using T = typename OT::T;
-  float sav[FM], sbv[FN][4];
-  with_scale_dtype(sad, [&](auto dt) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) sav[i] = scale_at<decltype(dt)::value>(sa, min(m0 + wm * WM + 16 * i + li, M - 1));
-  });
-  with_scale_dtype(sbd, [&](auto dt) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sbv[j][r] = scale_at<decltype(dt)::value>(sb, min(n0 + wn * WN + 16 * j + 4 * lg + r, N - 1));
-  });
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * WM + 16 * i + li;
-    if (m >= M) continue;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * WN + 16 * j + 4 * lg;
-      if (n >= N) continue;
-      T v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(acc[i][j][r] >> 8, sav[i], sbv[j][r]));
-      T* o = out + (int64_t)m * ldc + n;
-      if (n + 3 < N) {
-        if constexpr (sizeof(T) == 2) {
-          typedef short v4s __attribute__((ext_vector_type(4)));
-          v4s pk;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
-          *reinterpret_cast<v4s*>(o) = pk;
-        } else {
-          *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n + r < N) o[r] = v[r];
-      }
-    }
-  }
+  store_c_blocks<FM, FN, OT>(acc, sa, sad, sb, sbd, out, ldc, M, N, m0 + wm * WM, n0 + wn * WN, li, lg);
 }
 
 // ---------------------------------------------------------------------------
