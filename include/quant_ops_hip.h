@@ -105,6 +105,21 @@ int qo_int4_gemm(const int32_t* a, int64_t lda,
                  int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
+ * qo_int4_gemm followed by the bias of the W4A4 linear layer, fused into the
+ * epilogue: out[m, n] = rnd(rnd((acc * sa[m]) * sb[n]) + bias[n]), with bias
+ * in out_dtype (N elements, not NULL). The two roundings are those of the
+ * reference's `output + bias.to(dtype)` after the GEMM
+ * (w4a4_flatquant_dynamic.py:262-264 on int4_matmul's output).
+ */
+int qo_int4_gemm_bias(const int32_t* a, int64_t lda,
+                      const int32_t* b, int64_t b_stride_p, int64_t b_stride_n,
+                      const void* scale_a, int scale_a_dtype,
+                      const void* scale_b, int scale_b_dtype,
+                      const void* bias,
+                      void* out, int out_dtype, int64_t ldc,
+                      int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
  * Dequantize int4 codes: out[t, f] = float(q[t, f]) * float(scales[t]) (float32).
  *
  * Replaces dequantize_int4 (flatquant/ops.py:156-178), which the reference runs

@@ -19,7 +19,7 @@ STATUS = {0: "QO_OK", 1: "QO_ERR_NULL_POINTER", 2: "QO_ERR_SHAPE", 3: "QO_ERR_DT
 
 # Every symbol the header declares; the CPU tests check they are all exported.
 EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_flatquant_quantize",
-            "qo_int4_gemm", "qo_dequantize_int4", "qo_pack_int4_to_int32", "qo_unpack_int32_to_int4",
+            "qo_int4_gemm", "qo_int4_gemm_bias", "qo_dequantize_int4", "qo_pack_int4_to_int32", "qo_unpack_int32_to_int4",
             "qo_transpose_int32")
 
 _TORCH_CODE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
@@ -55,6 +55,9 @@ def lib():
     L.qo_int4_gemm.restype = c_int
     L.qo_int4_gemm.argtypes = [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_int, c_vp, c_int, c_vp, c_int, c_i64,
                                c_i64, c_i64, c_i64, c_vp]
+    L.qo_int4_gemm_bias.restype = c_int
+    L.qo_int4_gemm_bias.argtypes = [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int,
+                                    c_i64, c_i64, c_i64, c_i64, c_vp]
     L.qo_dequantize_int4.restype = c_int
     L.qo_dequantize_int4.argtypes = [c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_vp, c_vp]
     for name in ("qo_pack_int4_to_int32", "qo_unpack_int32_to_int4", "qo_transpose_int32"):
@@ -107,8 +110,9 @@ def flatquant_quantize(x, left, right, clip_ratio=1.0, pack_int32=False, out_cod
     return out_codes, out_scales
 
 
-def int4_gemm(a, b, scale_a, scale_b, out_dtype=torch.float16, out=None, stream=None):
-    """Call ``qo_int4_gemm``; ``b`` may be row-major [K/8, N] or the ``W.t()`` view."""
+def int4_gemm(a, b, scale_a, scale_b, out_dtype=torch.float16, out=None, stream=None, bias=None):
+    """Call ``qo_int4_gemm`` (``qo_int4_gemm_bias`` with ``bias``, converted to the
+    output dtype); ``b`` may be row-major [K/8, N] or the ``W.t()`` view."""
     m, kp = a.shape
     if a.stride(1) != 1:
         a = a.contiguous()
@@ -118,13 +122,17 @@ def int4_gemm(a, b, scale_a, scale_b, out_dtype=torch.float16, out=None, stream=
     n = b.shape[1]
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=a.device)
-    _check(lib().qo_int4_gemm(
-        ctypes.c_void_p(a.data_ptr()), a.stride(0) if m else kp,
-        ctypes.c_void_p(b.data_ptr()), b.stride(0), b.stride(1),
-        ctypes.c_void_p(scale_a.data_ptr()), _TORCH_CODE[scale_a.dtype],
-        ctypes.c_void_p(scale_b.data_ptr()), _TORCH_CODE[scale_b.dtype],
-        ctypes.c_void_p(out.data_ptr()), _TORCH_CODE[out.dtype], out.stride(0) if m else n,
-        m, n, kp * 8, _stream(stream)))
+    head = (ctypes.c_void_p(a.data_ptr()), a.stride(0) if m else kp,
+            ctypes.c_void_p(b.data_ptr()), b.stride(0), b.stride(1),
+            ctypes.c_void_p(scale_a.data_ptr()), _TORCH_CODE[scale_a.dtype],
+            ctypes.c_void_p(scale_b.data_ptr()), _TORCH_CODE[scale_b.dtype])
+    tail = (ctypes.c_void_p(out.data_ptr()), _TORCH_CODE[out.dtype], out.stride(0) if m else n,
+            m, n, kp * 8, _stream(stream))
+    if bias is None:
+        _check(lib().qo_int4_gemm(*head, *tail))
+    else:
+        bias = bias.to(out.dtype).contiguous()
+        _check(lib().qo_int4_gemm_bias(*head, ctypes.c_void_p(bias.data_ptr()), *tail))
     return out
 
 

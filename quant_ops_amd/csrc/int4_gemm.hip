@@ -54,6 +54,14 @@ __device__ inline float scale_out(int acc, float sa, float sb) {
   return v;
 }
 
+// Optional bias in the output type, added to the rounded output as the
+// reference's `output + bias.to(dtype)` does (one float32 add of the two
+// output-type values, one rounding back).
+template <class OT>
+__device__ inline typename OT::T add_bias(typename OT::T v, const typename OT::T* bias, int64_t n) {
+  return bias ? OT::cvt((float)v + (float)bias[n]) : v;
+}
+
 // ---------------------------------------------------------------------------
 // Generic kernel.
 // ---------------------------------------------------------------------------
@@ -61,7 +69,8 @@ template <class OT>
 __global__ void __launch_bounds__(256)
 gemm_i4_generic(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t bsp,
                 int64_t bsn, const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
-                typename OT::T* __restrict__ out, int64_t ldc, int64_t M, int64_t N, int64_t KP) {
+                typename OT::T* __restrict__ out, int64_t ldc, const typename OT::T* __restrict__ bias, int64_t M,
+                int64_t N, int64_t KP) {
   const int64_t n = (int64_t)blockIdx.x * 16 + (threadIdx.x & 15);
   const int64_t m = (int64_t)blockIdx.y * 16 + (threadIdx.x >> 4);
   if (m >= M || n >= N) return;
@@ -73,7 +82,7 @@ gemm_i4_generic(const int32_t* __restrict__ a, int64_t lda, const int32_t* __res
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc += nib(wa, i) * nib(wb, i);
   }
-  out[m * ldc + n] = OT::cvt(scale_out(acc, load_scale(sa, sad, m), load_scale(sb, sbd, n)));
+  out[m * ldc + n] = add_bias<OT>(OT::cvt(scale_out(acc, load_scale(sa, sad, m), load_scale(sb, sbd, n))), bias, n);
 }
 
 // ---------------------------------------------------------------------------
@@ -109,7 +118,8 @@ template <int BM, int BN, int BK, int WGM, int WGN, bool B_NK, class OT>
 __global__ void __launch_bounds__(64 * WGM * WGN, 1)
 gemm_i4_mfma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
              const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
-             typename OT::T* __restrict__ out, int64_t ldc, int M, int N, int K, int tiles_m, int tiles_n) {
+             typename OT::T* __restrict__ out, int64_t ldc, const typename OT::T* __restrict__ bias, int M, int N, int K,
+             int tiles_m, int tiles_n) {
   using C = GemmCfg<BM, BN, BK, WGM, WGN>;
   constexpr int NT = C::THREADS;
   constexpr int BKW = C::BKW, ROW = C::ROW, FM = C::FM, FN = C::FN;
@@ -265,7 +275,7 @@ gemm_i4_mfma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restri
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int nn = n + r < N ? n + r : N - 1;
-        v[r] = OT::cvt(scale_out(acc[i][j][r] >> 8, s_a, load_scale(sb, sbd, nn)));
+        v[r] = add_bias<OT>(OT::cvt(scale_out(acc[i][j][r] >> 8, s_a, load_scale(sb, sbd, nn))), bias, nn);
       }
       T* o = out + (int64_t)m * ldc + n;
       if (n + 3 < N) {
@@ -368,8 +378,8 @@ __device__ inline void with_scale_dtype(int code, F&& f) {
 // adjacent outputs; rows and columns past the matrix edge are skipped.
 template <int FM, int FN, class OT>
 __device__ inline void store_c_blocks(const v4i (&acc)[FM][FN], const void* sa, int sad, const void* sb, int sbd,
-                                      typename OT::T* out, int64_t ldc, int M, int N, int mrow, int ncol, int li,
-                                      int lg) {
+                                      typename OT::T* out, int64_t ldc, const typename OT::T* bias, int M, int N,
+                                      int mrow, int ncol, int li, int lg) {
   using T = typename OT::T;
   float sav[FM], sbv[FN][4];
   with_scale_dtype(sad, [&](auto dt) {
@@ -393,7 +403,8 @@ __device__ inline void store_c_blocks(const v4i (&acc)[FM][FN], const void* sa, 
       if (n >= N) continue;
       T v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(acc[i][j][r] >> 8, sav[i], sbv[j][r]));
+      for (int r = 0; r < 4; ++r)
+        v[r] = add_bias<OT>(OT::cvt(scale_out(acc[i][j][r] >> 8, sav[i], sbv[j][r])), bias, min(n + r, N - 1));
       T* o = out + (int64_t)m * ldc + n;
       if (n + 3 < N) {
         if constexpr (sizeof(T) == 2) {
@@ -418,7 +429,8 @@ template <int BM, int BN, int WGM, int WGN, int STAGES, bool B_NK, class OT>
 __global__ void __launch_bounds__(64 * WGM * WGN, 1)
 gemm_i4_dma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
             const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
-            typename OT::T* __restrict__ out, int64_t ldc, int M, int N, int K, int tiles_m) {
+            typename OT::T* __restrict__ out, int64_t ldc, const typename OT::T* __restrict__ bias, int M, int N,
+            int K, int tiles_m) {
   using S = DmaStage<BM, BN, B_NK>;
   constexpr int W = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -557,7 +569,7 @@ gemm_i4_dma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restric
   }
   gemm_wait_vmcnt<0>();
 
-  store_c_blocks<FM, FN, OT>(acc, sa, sad, sb, sbd, out, ldc, M, N, m0 + wm * WM, n0 + wn * WN, li, lg);
+  store_c_blocks<FM, FN, OT>(acc, sa, sad, sb, sbd, out, ldc, bias, M, N, m0 + wm * WM, n0 + wn * WN, li, lg);
 }
 
 // ---------------------------------------------------------------------------
@@ -575,7 +587,8 @@ template <int BM, int BN, int WGM, int WGN, int STAGES, bool B_NK, class OT>
 __global__ void __launch_bounds__(64 * WGM * WGN, 1)
 gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
            const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
-           typename OT::T* __restrict__ out, int64_t ldc, int M, int N, int K, int tiles_m) {
+           typename OT::T* __restrict__ out, int64_t ldc, const typename OT::T* __restrict__ bias, int M, int N,
+           int K, int tiles_m) {
   using S = DmaStage<BM, BN, B_NK>;
   constexpr int W = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -719,7 +732,7 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
   }
   gemm_wait_vmcnt<0>();
 
-  store_c_blocks<FM, FN, OT>(acc, sa, sad, sb, sbd, out, ldc, M, N, m0 + wm * WM, n0 + wn * WN, li, lg);
+  store_c_blocks<FM, FN, OT>(acc, sa, sad, sb, sbd, out, ldc, bias, M, N, m0 + wm * WM, n0 + wn * WN, li, lg);
 }
 
 // ---------------------------------------------------------------------------
@@ -744,7 +757,8 @@ template <int MT, bool B_NK, class OT>
 __global__ void __launch_bounds__(512)
 gemm_i4_skinny(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
                const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
-               typename OT::T* __restrict__ out, int64_t ldc, int M, int N, int K) {
+               typename OT::T* __restrict__ out, int64_t ldc, const typename OT::T* __restrict__ bias, int M, int N,
+               int K) {
   constexpr int CH = SkinnyCfg<MT, B_NK, OT>::CH;
   __shared__ __align__(16) v4i part[8][MT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -824,7 +838,9 @@ gemm_i4_skinny(const int32_t* __restrict__ a, int64_t lda, const int32_t* __rest
   const float sam = load_scale(sa, sad, m);
   T v[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(sum[r] >> 8, sam, load_scale(sb, sbd, min(nc + r, N - 1))));
+  for (int r = 0; r < 4; ++r)
+    v[r] = add_bias<OT>(OT::cvt(scale_out(sum[r] >> 8, sam, load_scale(sb, sbd, min(nc + r, N - 1)))), bias,
+                        min(nc + r, N - 1));
   T* o = out + (int64_t)m * ldc + nc;
   if (nc + 3 < N) {
     if constexpr (sizeof(T) == 2) {
@@ -856,20 +872,20 @@ static bool gemm_allow_dma() {
 
 template <class OT>
 static void launch_generic(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, int64_t bsn,
-                           const void* sa, int sad, const void* sb, int sbd, void* out, int64_t ldc, int64_t M,
+                           const void* sa, int sad, const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int64_t M,
                            int64_t N, int64_t K, hipStream_t stream) {
   dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
   hipLaunchKernelGGL(gemm_i4_generic<OT>, grid, dim3(256), 0, stream, a, lda, b, bsp, bsn, sa, sad, sb, sbd,
-                     reinterpret_cast<typename OT::T*>(out), ldc, M, N, K / 8);
+                     reinterpret_cast<typename OT::T*>(out), ldc, reinterpret_cast<const typename OT::T*>(bias), M, N, K / 8);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool B_NK, class OT>
 static void launch_mfma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
-                        const void* sb, int sbd, void* out, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+                        const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K, hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   hipLaunchKernelGGL((gemm_i4_mfma<BM, BN, BK, WGM, WGN, B_NK, OT>), dim3(tiles_m * tiles_n),
                      dim3(64 * WGM * WGN), 0, stream, a, lda,
-                     b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, M, N, K, tiles_m,
+                     b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, reinterpret_cast<const typename OT::T*>(bias), M, N, K, tiles_m,
                      tiles_n);
 }
 
@@ -879,14 +895,14 @@ static void launch_mfma(const int32_t* a, int64_t lda, const int32_t* b, int64_t
 // operand would not fit a second register set within 256 VGPRs.
 template <int BM, int BN, bool B_NK, class OT>
 static void launch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
-                       const void* sb, int sbd, void* out, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+                       const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K, hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   if constexpr (B_NK)
     hipLaunchKernelGGL((gemm_i4_pp<BM, BN, 4, 2, 4, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a,
-                       lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, M, N, K, tiles_m);
+                       lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, reinterpret_cast<const typename OT::T*>(bias), M, N, K, tiles_m);
   else
     hipLaunchKernelGGL((gemm_i4_dma<BM, BN, 4, 2, 4, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a,
-                       lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, M, N, K, tiles_m);
+                       lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, reinterpret_cast<const typename OT::T*>(bias), M, N, K, tiles_m);
 }
 
 // Fraction of the machine's workgroup slots doing useful output in a launch
@@ -913,12 +929,12 @@ static int gemm_cu_count() {
 
 template <bool B_NK, class OT>
 static void dispatch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
-                         const void* sb, int sbd, void* out, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+                         const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K, hipStream_t stream) {
   const int cus = gemm_cu_count();
   if (tile_efficiency(M, N, 256, 224, cus) > tile_efficiency(M, N, 256, 256, cus))
-    launch_dma<256, 224, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, M, N, K, stream);
+    launch_dma<256, 224, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
   else
-    launch_dma<256, 256, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, M, N, K, stream);
+    launch_dma<256, 256, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
 }
 
 // QO_GEMM_NO_SKINNY=1 sends small M to the tiled kernels (tests use it to
@@ -930,13 +946,13 @@ static bool gemm_allow_skinny() {
 
 template <class OT>
 static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, bool b_nk, const void* sa,
-                          int sad, const void* sb, int sbd, void* out, int64_t ldc, int M, int N, int K,
+                          int sad, const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K,
                           hipStream_t stream) {
   const dim3 grid((unsigned)((N + 15) / 16));
   using T = typename OT::T;
   auto go = [&](auto mt, auto nk_layout) {
     hipLaunchKernelGGL((gemm_i4_skinny<decltype(mt)::value, decltype(nk_layout)::value, OT>), grid, dim3(512), 0,
-                       stream, a, lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, M, N, K);
+                       stream, a, lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
   };
   auto by_layout = [&](auto mt) {
     if (b_nk) go(mt, std::true_type{});
@@ -951,7 +967,7 @@ static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64
 
 template <class OT>
 static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, int64_t bsn, const void* sa,
-                     int sad, const void* sb, int sbd, void* out, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                     int sad, const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int64_t M, int64_t N, int64_t K,
                      hipStream_t stream, bool allow_fast) {
   using T = typename OT::T;
   const bool b_nk = (bsp == 1);
@@ -966,24 +982,24 @@ static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bs
     const int m = (int)M, n = (int)N, k = (int)K;
     // decode shapes: the skinny kernel (columns x K-slices, B streamed once)
     if (m <= 64 && k % 128 == 0 && k > 0 && gemm_allow_skinny()) {
-      launch_skinny<OT>(a, lda, b, ldb, b_nk, sa, sad, sb, sbd, out, ldc, m, n, k, stream);
+      launch_skinny<OT>(a, lda, b, ldb, b_nk, sa, sad, sb, sbd, out, ldc, bias, m, n, k, stream);
       return;
     }
     // pipelined kernel: whole 128-deep stages; KN rows read as 16-byte column groups
     if (k % 128 == 0 && k > 0 && (b_nk || n % 4 == 0) && gemm_allow_dma()) {
       if (b_nk)
-        dispatch_dma<true, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, m, n, k, stream);
+        dispatch_dma<true, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, m, n, k, stream);
       else
-        dispatch_dma<false, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, m, n, k, stream);
+        dispatch_dma<false, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, m, n, k, stream);
       return;
     }
     if (b_nk)
-      launch_mfma<QO_GEMM_TILE, true, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, m, n, k, stream);
+      launch_mfma<QO_GEMM_TILE, true, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, m, n, k, stream);
     else
-      launch_mfma<QO_GEMM_TILE, false, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, m, n, k, stream);
+      launch_mfma<QO_GEMM_TILE, false, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, m, n, k, stream);
     return;
   }
-  launch_generic<OT>(a, lda, b, bsp, bsn, sa, sad, sb, sbd, out, ldc, M, N, K, stream);
+  launch_generic<OT>(a, lda, b, bsp, bsn, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
 }
 
 }  // namespace qo
@@ -997,33 +1013,32 @@ static bool gemm_allow_fast() {
 
 static bool is_float_code(int d) { return d == QO_DTYPE_F32 || d == QO_DTYPE_F16 || d == QO_DTYPE_BF16; }
 
-extern "C" int qo_int4_gemm(const int32_t* a, int64_t lda, const int32_t* b, int64_t b_stride_p,
-                            int64_t b_stride_n, const void* scale_a, int scale_a_dtype, const void* scale_b,
-                            int scale_b_dtype, void* out, int out_dtype, int64_t ldc, int64_t M, int64_t N,
-                            int64_t K, void* stream) {
+static int gemm_entry(const char* who, const int32_t* a, int64_t lda, const int32_t* b, int64_t b_stride_p,
+                      int64_t b_stride_n, const void* scale_a, int scale_a_dtype, const void* scale_b,
+                      int scale_b_dtype, void* out, int out_dtype, int64_t ldc, const void* bias, int64_t M,
+                      int64_t N, int64_t K, void* stream) {
   using namespace qo;
   if (M < 0 || N < 0 || K < 0 || (K % 8) != 0) {
-    qo_set_error("qo_int4_gemm: invalid sizes M=%lld N=%lld K=%lld (K must be a multiple of 8)", (long long)M,
+    qo_set_error("%s: invalid sizes M=%lld N=%lld K=%lld (K must be a multiple of 8)", who, (long long)M,
                  (long long)N, (long long)K);
     return QO_ERR_SHAPE;
   }
   if (K >= (int64_t(1) << 21)) {
-    qo_set_error("qo_int4_gemm: K=%lld exceeds the exact int32 accumulation range (K < 2^21)", (long long)K);
+    qo_set_error("%s: K=%lld exceeds the exact int32 accumulation range (K < 2^21)", who, (long long)K);
     return QO_ERR_SHAPE;
   }
   if (lda < K / 8 || ldc < N) {
-    qo_set_error("qo_int4_gemm: leading dimensions too small (lda=%lld, ldc=%lld)", (long long)lda,
-                 (long long)ldc);
+    qo_set_error("%s: leading dimensions too small (lda=%lld, ldc=%lld)", who, (long long)lda, (long long)ldc);
     return QO_ERR_SHAPE;
   }
   if (!is_float_code(scale_a_dtype) || !is_float_code(scale_b_dtype) || !is_float_code(out_dtype)) {
-    qo_set_error("qo_int4_gemm: unsupported dtype codes (scale_a=%d, scale_b=%d, out=%d)", scale_a_dtype,
+    qo_set_error("%s: unsupported dtype codes (scale_a=%d, scale_b=%d, out=%d)", who, scale_a_dtype,
                  scale_b_dtype, out_dtype);
     return QO_ERR_DTYPE;
   }
   if (M == 0 || N == 0) return QO_OK;
   if (!a || !b || !scale_a || !scale_b || !out) {
-    qo_set_error("qo_int4_gemm: NULL pointer argument");
+    qo_set_error("%s: NULL pointer argument", who);
     return QO_ERR_NULL_POINTER;
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -1031,21 +1046,41 @@ extern "C" int qo_int4_gemm(const int32_t* a, int64_t lda, const int32_t* b, int
   switch (out_dtype) {
     case QO_DTYPE_F16:
       dispatch<OutF16>(a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b, scale_b_dtype, out, ldc,
-                       M, N, K, s, fast);
+                       bias, M, N, K, s, fast);
       break;
     case QO_DTYPE_BF16:
       dispatch<OutBF16>(a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b, scale_b_dtype, out,
-                        ldc, M, N, K, s, fast);
+                        ldc, bias, M, N, K, s, fast);
       break;
     default:
       dispatch<OutF32>(a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b, scale_b_dtype, out, ldc,
-                       M, N, K, s, fast);
+                       bias, M, N, K, s, fast);
       break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
-    qo_set_error("qo_int4_gemm: launch failed: %s", hipGetErrorString(e));
+    qo_set_error("%s: launch failed: %s", who, hipGetErrorString(e));
     return QO_ERR_LAUNCH;
   }
   return QO_OK;
+}
+
+extern "C" int qo_int4_gemm(const int32_t* a, int64_t lda, const int32_t* b, int64_t b_stride_p,
+                            int64_t b_stride_n, const void* scale_a, int scale_a_dtype, const void* scale_b,
+                            int scale_b_dtype, void* out, int out_dtype, int64_t ldc, int64_t M, int64_t N,
+                            int64_t K, void* stream) {
+  return gemm_entry("qo_int4_gemm", a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b,
+                    scale_b_dtype, out, out_dtype, ldc, nullptr, M, N, K, stream);
+}
+
+extern "C" int qo_int4_gemm_bias(const int32_t* a, int64_t lda, const int32_t* b, int64_t b_stride_p,
+                                 int64_t b_stride_n, const void* scale_a, int scale_a_dtype, const void* scale_b,
+                                 int scale_b_dtype, const void* bias, void* out, int out_dtype, int64_t ldc,
+                                 int64_t M, int64_t N, int64_t K, void* stream) {
+  if (!bias && M > 0 && N > 0) {
+    qo_set_error("qo_int4_gemm_bias: NULL bias (use qo_int4_gemm for no bias)");
+    return QO_ERR_NULL_POINTER;
+  }
+  return gemm_entry("qo_int4_gemm_bias", a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b,
+                    scale_b_dtype, out, out_dtype, ldc, bias, M, N, K, stream);
 }

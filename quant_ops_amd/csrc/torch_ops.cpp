@@ -78,7 +78,8 @@ std::tuple<at::Tensor, at::Tensor> flatquant_dynamic_quantize(const at::Tensor& 
 // may also be float16 / bfloat16 (the fallback promotes them), and b may be the
 // transposed view of a [N, K/8] weight.
 at::Tensor int4_matmul_impl(const at::Tensor& a, const at::Tensor& b, const at::Tensor& scale_a,
-                            const at::Tensor& scale_b, at::ScalarType out_dtype) {
+                            const at::Tensor& scale_b, at::ScalarType out_dtype,
+                            const std::optional<at::Tensor>& bias = std::nullopt) {
   TORCH_CHECK(a.is_cuda(), "a_packed must be on CUDA");
   TORCH_CHECK(b.is_cuda(), "b_packed must be on CUDA");
   TORCH_CHECK(scale_a.is_cuda(), "scale_a must be on CUDA");
@@ -106,6 +107,16 @@ at::Tensor int4_matmul_impl(const at::Tensor& a, const at::Tensor& b, const at::
   if (KP == 1) bsp = 1;     // a single packed row: either stride works
   if (N == 1) bsn = 1;
   const int64_t lda = M > 0 ? A.stride(0) : KP;
+  if (bias.has_value()) {
+    TORCH_CHECK(bias->is_cuda() && bias->numel() == N, "bias must be a GPU tensor of N elements");
+    // the reference adds bias.to(output dtype) to the output
+    at::Tensor bv = bias->to(out_dtype).contiguous();
+    check_status(qo_int4_gemm_bias(A.data_ptr<int32_t>(), lda, B.data_ptr<int32_t>(), bsp, bsn, sa.data_ptr(), sad,
+                                   sb.data_ptr(), sbd, bv.data_ptr(), out.data_ptr(), od, N, M, N, K,
+                                   current_stream(a)),
+                 "int4_matmul_bias");
+    return out;
+  }
   check_status(qo_int4_gemm(A.data_ptr<int32_t>(), lda, B.data_ptr<int32_t>(), bsp, bsn, sa.data_ptr(), sad,
                             sb.data_ptr(), sbd, out.data_ptr(), od, N, M, N, K, current_stream(a)),
                "int4_matmul");
@@ -120,6 +131,12 @@ at::Tensor int4_matmul(const at::Tensor& a, const at::Tensor& b, const at::Tenso
 at::Tensor int4_matmul_ex(const at::Tensor& a, const at::Tensor& b, const at::Tensor& scale_a,
                           const at::Tensor& scale_b, std::optional<at::ScalarType> out_dtype) {
   return int4_matmul_impl(a, b, scale_a, scale_b, out_dtype.value_or(at::kHalf));
+}
+
+at::Tensor int4_matmul_bias(const at::Tensor& a, const at::Tensor& b, const at::Tensor& scale_a,
+                            const at::Tensor& scale_b, const at::Tensor& bias,
+                            std::optional<at::ScalarType> out_dtype) {
+  return int4_matmul_impl(a, b, scale_a, scale_b, out_dtype.value_or(at::kHalf), bias);
 }
 
 at::Tensor dequantize_int4(const at::Tensor& quantized, const at::Tensor& scales, bool packed_int32) {
@@ -151,6 +168,9 @@ TORCH_LIBRARY(quant_ops, m) {
   m.def("int4_matmul(Tensor a, Tensor b, Tensor scale_a, Tensor scale_b) -> Tensor");
   m.def("int4_matmul_ex(Tensor a, Tensor b, Tensor scale_a, Tensor scale_b, ScalarType? out_dtype=None) -> Tensor");
   m.def("dequantize_int4(Tensor quantized, Tensor scales, bool packed_int32=False) -> Tensor");
+  m.def(
+      "int4_matmul_bias(Tensor a, Tensor b, Tensor scale_a, Tensor scale_b, Tensor bias, "
+      "ScalarType? out_dtype=None) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(quant_ops, CUDA, m) {
@@ -158,4 +178,5 @@ TORCH_LIBRARY_IMPL(quant_ops, CUDA, m) {
   m.impl("int4_matmul", &int4_matmul);
   m.impl("int4_matmul_ex", &int4_matmul_ex);
   m.impl("dequantize_int4", &dequantize_int4);
+  m.impl("int4_matmul_bias", &int4_matmul_bias);
 }

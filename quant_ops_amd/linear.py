@@ -9,7 +9,8 @@ Mirrors the reference's vLLM linear method
 * ``w4a4_flatquant_linear`` is ``apply`` (``:168-266``): per-token dynamic
   quantization of x with the Kronecker transform, the int4 GEMM against the
   packed weight's ``.t()`` view with per-token x per-channel scales, output in
-  x's dtype, then ``+ bias``.
+  x's dtype, then ``+ bias`` (on the GPU fused into the GEMM epilogue with the
+  same two roundings).
 
 Differences, each deliberate:
 
@@ -26,6 +27,7 @@ from typing import Optional
 
 import torch
 
+from . import _loader
 from .flatquant import flatquant_dynamic_quantize
 from .int4_matmul import int4_matmul, pack_int4_to_int32
 
@@ -58,9 +60,13 @@ def w4a4_flatquant_linear(
     dtype = x.dtype
     codes, act_scale = flatquant_dynamic_quantize(
         x.reshape(-1, in_features), left_trans.to(dtype), right_trans.to(dtype), clip_ratio, pack_int32=True)
-    out = int4_matmul(codes, weight_packed.t(), act_scale.to(torch.float32),
-                      weight_scale.reshape(-1).to(torch.float32), out_dtype=dtype)
-    out = out.view(*x.shape[:-1], out_features)
-    if bias is not None:
-        out = out + bias.to(dtype)
-    return out
+    sa, sb = act_scale.to(torch.float32), weight_scale.reshape(-1).to(torch.float32)
+    if bias is not None and codes.is_cuda:
+        # bias fused into the GEMM epilogue, with the same two roundings
+        _loader.require_kernels("w4a4_flatquant_linear")
+        out = torch.ops.quant_ops.int4_matmul_bias(codes, weight_packed.t(), sa, sb, bias.to(dtype), dtype)
+    else:
+        out = int4_matmul(codes, weight_packed.t(), sa, sb, out_dtype=dtype)
+        if bias is not None:
+            out = out + bias.to(dtype)
+    return out.view(*x.shape[:-1], out_features)

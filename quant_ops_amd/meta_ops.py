@@ -20,6 +20,13 @@ if _loader.KERNELS_AVAILABLE:
     def _int4_matmul_ex_fake(a, b, scale_a, scale_b, out_dtype=None):
         return a.new_empty((a.size(0), b.size(1)), dtype=out_dtype or torch.float16)
 
+    # defined by libraries built from this version on (a stale build lacks it)
+    if hasattr(torch.ops.quant_ops, "int4_matmul_bias"):
+
+        @torch.library.register_fake("quant_ops::int4_matmul_bias")
+        def _int4_matmul_bias_fake(a, b, scale_a, scale_b, bias, out_dtype=None):
+            return a.new_empty((a.size(0), b.size(1)), dtype=out_dtype or torch.float16)
+
     @torch.library.register_fake("quant_ops::flatquant_dynamic_quantize")
     def _flatquant_fake(input_tensor, left_trans, right_trans, clip_ratio=1.0, pack_int32=False):
         tokens, feats = input_tensor.shape

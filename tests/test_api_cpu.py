@@ -200,6 +200,11 @@ def test_fake_kernels_give_reference_shapes():
     from torch._subclasses.fake_tensor import FakeTensorMode
 
     with FakeTensorMode():
+        a = torch.empty(5, 16, dtype=torch.int32)
+        b = torch.empty(16, 9, dtype=torch.int32)
+        o = torch.ops.quant_ops.int4_matmul_bias(a, b, torch.empty(5), torch.empty(9), torch.empty(9),
+                                                 torch.bfloat16)
+        assert o.shape == (5, 9) and o.dtype == torch.bfloat16
         x = torch.empty(6, 64, dtype=torch.float16)
         L = torch.empty(8, 8, dtype=torch.float16)
         q, s = torch.ops.quant_ops.flatquant_dynamic_quantize(x, L, L, 0.9, True)

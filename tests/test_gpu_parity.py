@@ -377,6 +377,30 @@ def test_gemm_scale_and_out_dtypes(gpu, sdt, odt):
     assert out.dtype == odt and torch.equal(out.cpu(), ref)
 
 
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("path,m,n,k,bview", [
+    ("skinny", 16, 300, 1024, True), ("tiled", 300, 260, 2048, False), ("tiled", 257, 516, 1024, True),
+    ("mfma", 96, 160, 544, False), ("generic", 33, 70, 136, True)])
+def test_gemm_bias_fused_bit_exact(gpu, odt, path, m, n, k, bview, monkeypatch):
+    """The bias epilogue of every GEMM path equals the reference's separate
+    `output + bias.to(dtype)` after int4_matmul: two roundings to the output
+    dtype (w4a4_flatquant_dynamic.py:262-264)."""
+    case = wl.gemm_case(m, n, k, seed=7 * m + n, b_transposed_view=bview)
+    g = torch.Generator().manual_seed(m + k)
+    bias = (torch.randn(n, generator=g) * 4).to(torch.bfloat16)   # converted to odt as the reference does
+    if path == "generic":
+        monkeypatch.setenv("QO_GEMM_FORCE_GENERIC", "1")
+    _say(f"gemm bias {path} {m}x{n}x{k} bview={bview} {odt}")
+    out = capi.int4_gemm(case.a.to(gpu), case.b.to(gpu), case.scale_a.to(gpu), case.scale_b.to(gpu),
+                         out_dtype=odt, bias=bias.to(gpu))
+    op = torch.ops.quant_ops.int4_matmul_bias(case.a.to(gpu), case.b.to(gpu), case.scale_a.to(gpu),
+                                              case.scale_b.to(gpu), bias.to(gpu), odt)
+    torch.cuda.synchronize()
+    ref = oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b, out_dtype=odt) + bias.to(odt)
+    assert out.dtype == odt and torch.equal(out.cpu(), ref)
+    assert torch.equal(op.cpu(), ref)
+
+
 def test_gemm_fast_matches_generic(gpu, monkeypatch):
     case = wl.gemm_case(512, 384, 2048, seed=12, b_transposed_view=True)
     args = (case.a.to(gpu), case.b.to(gpu), case.scale_a.to(gpu), case.scale_b.to(gpu))
