@@ -445,6 +445,57 @@ def test_gemm_rejects_bad_shapes(gpu):
         qo.int4_matmul(a.float(), b, torch.ones(4, device=gpu), torch.ones(5, device=gpu))
 
 
+# --------------------------------------------------------------------------- sizes past 2^31 elements
+
+@pytest.mark.parametrize("mn,dtype", [((64, 64), torch.float16), ((112, 128), torch.bfloat16)])
+def test_quantize_beyond_2g_elements(gpu, mn, dtype):
+    """X with more than 2^31 elements (4+ GB): every offset is 64-bit. Tokens
+    are independent, so sampled tokens (the first, middle and last among them)
+    must come out bit for bit as when the same rows are quantized on their own
+    (the parity of which the other tests establish), and within the parity bar
+    of the oracle."""
+    m, n = mn
+    f = m * n
+    t = 2**31 // f + 300
+    g = torch.Generator(device=gpu).manual_seed(91)
+    x = torch.randn(t, f, generator=g, device=gpu, dtype=torch.float32).to(dtype)
+    L, R = wl.orthogonal(m, 92, dtype).to(gpu), wl.orthogonal(n, 93, dtype).to(gpu)
+    _say(f"quantize {t} x {f} {dtype} ({t * f / 2**31:.2f} x 2^31 elements)")
+    q, s = capi.flatquant_quantize(x, L, R, 0.9, True)
+    torch.cuda.synchronize()
+    gi = torch.Generator().manual_seed(94)
+    idx = torch.cat([torch.tensor([0, 1, t // 2, t - 2, t - 1]), torch.randint(0, t, (59,), generator=gi)])
+    idx_d = idx.to(gpu)
+    rows = x[idx_d].contiguous()
+    q_small, s_small = capi.flatquant_quantize(rows, L, R, 0.9, True)
+    torch.cuda.synchronize()
+    assert torch.equal(q[idx_d], q_small) and torch.equal(s[idx_d], s_small)
+    q_ref, _ = ofq.flatquant_pytorch(rows.cpu(), L.cpu(), R.cpu(), 0.9, True)
+    d = (_codes_int8(q_small, True).int() - _codes_int8(q_ref, True).int()).abs()
+    assert int(d.max()) <= 1 and float((d != 0).float().mean()) <= CODE_FLIP_FRAC
+    del x, q, s
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("bview", [False, True])
+def test_gemm_beyond_2g_outputs(gpu, bview):
+    """An output of more than 2^31 elements (65552 x 32832 bf16): 64-bit output
+    offsets in the tiled kernels; sampled rows, including the last, bit-exact."""
+    m, n, k = 65552, 32832, 128
+    case = wl.gemm_case(64, n, k, seed=95, b_transposed_view=bview)     # B, sb from the seeded generator
+    g = torch.Generator().manual_seed(96)
+    a = wl.random_packed(m, k // 8, 97)
+    sa = wl.uniform(m, 0.01, 0.1, 98)
+    _say(f"gemm {m}x{n}x{k} bview={bview} ({m * n / 2**31:.2f} x 2^31 outputs)")
+    out = capi.int4_gemm(a.to(gpu), case.b.to(gpu), sa.to(gpu), case.scale_b.to(gpu), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    idx = torch.cat([torch.tensor([0, m // 2, m - 1]), torch.randint(0, m, (29,), generator=g)])
+    ref = oi4.int4_matmul_pytorch(a[idx], case.b, sa[idx], case.scale_b, out_dtype=torch.bfloat16)
+    assert torch.equal(out[idx.to(gpu)].cpu(), ref)
+    del out
+    torch.cuda.empty_cache()
+
+
 # --------------------------------------------------------------------------- end to end (config 5)
 
 @pytest.mark.parametrize("tokens", [16, 4096])
