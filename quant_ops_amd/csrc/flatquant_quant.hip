@@ -1008,9 +1008,19 @@ struct DuoShape {
   // X buffers per slot: two (the next-but-one token's X is copied while this
   // one is processed) where the LDS holds them, else one
   static constexpr int XB = SLOTS * 2 * X_BYTES + LF_BYTES + 64 <= 160 * 1024 ? 2 : 1;
-  static constexpr int XAREA = SLOTS * XB * X_BYTES;
-  // LDS block: X area + L fragments, at least R's N*N elements (set-up staging)
-  static constexpr int LDS_BYTES = XAREA + LF_BYTES > N * N * 2 ? XAREA + LF_BYTES : N * N * 2;
+  static constexpr int XAREA = SLOTS * XB * X_BYTES;   // buffer b of slot p at (b SLOTS + p) X_BYTES
+  static constexpr int STAGE_BYTES = N * N * 2 + M * M * 2;   // R and L rows during the set-up
+  // EARLY: the set-up stages R and L behind the slots' first X buffers, so the
+  // first tokens' copies are issued before the set-up instead of after it
+  // (worth a global round trip when each slot has one or two tokens), where
+  // the LDS holds that layout; otherwise the staging reuses the X area.
+  static constexpr int EARLY_LF_OFF =
+      (SLOTS * X_BYTES + STAGE_BYTES > XAREA ? SLOTS * X_BYTES + STAGE_BYTES : XAREA);
+  static constexpr bool EARLY = EARLY_LF_OFF + LF_BYTES + 64 <= 160 * 1024;
+  static constexpr int STAGE_OFF = EARLY ? SLOTS * X_BYTES : 0;
+  static constexpr int LF_OFF = EARLY ? EARLY_LF_OFF : XAREA;
+  static constexpr int LDS_BYTES = LF_OFF + LF_BYTES;
+  static_assert(STAGE_OFF + STAGE_BYTES <= LF_OFF, "R and L staging space");
   static_assert(MB >= 2 && MB <= 8, "M = 32 .. 128");
   static_assert(XF % 2 == 0, "X fragments split over the pair");
 };
@@ -1030,12 +1040,12 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   // across both)
   __shared__ __align__(16) unsigned char lds_all[S::LDS_BYTES];
   __shared__ float red[SLOTS][2];
-  unsigned char* const lfs = lds_all + S::XAREA;
+  unsigned char* const lfs = lds_all + S::LF_OFF;
 
   const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int p = wave >> 1, c = wave & 1;   // token slot, column half
-  unsigned char* const xslot = lds_all + p * XB * S::X_BYTES;
+  auto xbuf = [&](int b) { return lds_all + (b * SLOTS + p) * S::X_BYTES; };
   // token of this wave's slot in iteration it
   const int64_t step = (int64_t)gridDim.x * SLOTS;
   const int64_t t0 = (int64_t)blockIdx.x * SLOTS + p;
@@ -1047,7 +1057,7 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   auto issue_x = [&](int64_t tt, int b) {
     tt = tt < tokens ? tt : tokens - 1;
     const T* base = x + tt * x_ld + li * N + 8 * lg;
-    const uint32_t lbase = lds_addr(xslot + b * S::X_BYTES);
+    const uint32_t lbase = lds_addr(xbuf(b));
 #pragma unroll
     for (int i = 0; i < S::XF / 2; ++i) {
       const int f = c + 2 * i;
@@ -1055,13 +1065,14 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     }
   };
 
-  // Set-up, once per workgroup. R and L are copied row-major into the X area
-  // by LDS-DMA (coalesced 16-byte chunks; R at the start, L after it, one
-  // round trip for both), then rearranged from LDS: R into this wave's
-  // registers, L into the L fragments.
-  static_assert(N * N * 2 + M * M * 2 <= S::XAREA, "R and L staging space");
+  // Set-up, once per workgroup. R and L are copied row-major into LDS by
+  // LDS-DMA (coalesced 16-byte chunks; R, then L after it, one round trip for
+  // both), then rearranged from LDS: R into this wave's registers, L into the
+  // L fragments. With EARLY the first token's X copy of each slot follows the
+  // staging copies, and the wait leaves it in flight.
+  unsigned char* const stage = lds_all + S::STAGE_OFF;
   {
-    const uint32_t lb = lds_addr(lds_all);
+    const uint32_t lb = lds_addr(stage);
     auto stage_rows = [&](const T* src, int chunks, uint32_t base) {   // chunk c (8 elements) -> base + 16 c
 #pragma unroll 1
       for (int c0 = wave * 64; c0 < chunks; c0 += 64 * 2 * SLOTS)
@@ -1069,14 +1080,19 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     };
     stage_rows(right, N * N / 8, lb);
     stage_rows(left, M * M / 8, lb + N * N * 2);
-    wait_vmcnt<0>();
+    if constexpr (S::EARLY) {
+      issue_x(t0, 0);
+      wait_vmcnt<S::XF / 2>();   // the staging copies (older) have landed
+    } else {
+      wait_vmcnt<0>();
+    }
     lds_barrier();
   }
   // R fragments of this wave's columns: rf[q][h][ks][j] = R[32ks + 8lg + j][n],
   // n = 64c + 16(li/4) + 8q + 4h + li%4.
   V rf[2][2][KS1];
   {
-    const T* rs = reinterpret_cast<const T*>(lds_all);
+    const T* rs = reinterpret_cast<const T*>(stage);
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
@@ -1092,7 +1108,7 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   // holds L[32s + 16(j/4) + 4(l/16) + j%4][16mb + l%16]; in the zero-padded
   // tail slab (s = KS2, M / 16 odd) elements 4..7 are zero.
   {
-    const T* ls = reinterpret_cast<const T*>(lds_all + N * N * 2);
+    const T* ls = reinterpret_cast<const T*>(stage + N * N * 2);
 #pragma unroll 1
     for (int fr = wave; fr < MB * S::KSL; fr += 2 * SLOTS) {
       const int mb = fr / S::KSL, sl = fr % S::KSL;
@@ -1106,14 +1122,14 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
       *reinterpret_cast<V*>(lfs + fr * 1024 + 16 * lane) = v;
     }
   }
-  lds_barrier();   // R in registers, L fragments written: the X area is free
+  lds_barrier();   // R in registers, L fragments written: the staging space is free
 #pragma unroll
-  for (int b = 0; b < XB; ++b) issue_x(t0 + b * step, b);
+  for (int b = S::EARLY ? 1 : 0; b < XB; ++b) issue_x(t0 + b * step, b);
 
   for (int64_t it = 0; t0 - p + it * step < tokens; ++it) {
     const int64_t t = t0 + it * step;
     const int b = XB == 2 ? (int)(it & 1) : 0;
-    unsigned char* const xb = xslot + b * S::X_BYTES;
+    unsigned char* const xb = xbuf(b);
     // This iteration's copy is older than the copies issued in the last
     // XB - 1 iterations. The output stores issued in between are not counted:
     // a store may complete out of order with the copies, and counting it
