@@ -288,6 +288,24 @@ def test_dequantize_bit_exact(gpu, pack, sdt):
     assert torch.equal(out.cpu(), ref) and torch.equal(out2.cpu(), ref)
 
 
+@pytest.mark.parametrize("t,f,misaligned", [(3, 2400, False), (70000, 64, False), (9, 4096, True)])
+def test_dequantize_packed_shapes(gpu, t, f, misaligned):
+    """Packed codes: rows that are not a multiple of the 256-word block, more
+    tokens than one launch row dimension (65535), and an output 4 bytes off
+    16-byte alignment (the one-output-per-thread path)."""
+    g = torch.Generator().manual_seed(t + f)
+    q = torch.randint(-8, 8, (t, f), generator=g, dtype=torch.int8)
+    s = (torch.rand(t, generator=g) + 0.01).to(torch.float16)
+    codes = torch.from_numpy(oi4.pack_int4_to_int32(q.numpy()))
+    big = torch.full((t * f + 4,), -1.0, device=gpu)
+    out = big[1:1 + t * f].view(t, f) if misaligned else big[:t * f].view(t, f)
+    _say(f"dequantize packed {t}x{f} misaligned={misaligned}")
+    capi.dequantize_int4(codes.to(gpu), s.to(gpu), True, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), ofq.dequantize_int4(codes, s, True))
+    assert float(big[0 if misaligned else t * f]) == -1.0   # nothing written outside the view
+
+
 def test_dequantize_odd_features(gpu):
     q = torch.randint(-8, 8, (5, 13), dtype=torch.int8)
     s = torch.rand(5) + 0.5
