@@ -1415,9 +1415,10 @@ static int run_quantize(const void* x, int64_t tokens, int64_t x_ld, const void*
                         int N, float clip, void* out_codes, float* out_scales, hipStream_t stream,
                         bool allow_mfma) {
   if constexpr (DT::code != QO_DTYPE_F32) {
-    // 16-byte vector loads of X rows and of L / R rows
+    // 16-byte vector loads of X rows and of L / R rows, vector stores of codes
     const bool aligned = ((uintptr_t)x % 16 == 0) && ((x_ld * (int64_t)sizeof(typename DT::T)) % 16 == 0) &&
-                         ((uintptr_t)left % 16 == 0) && ((uintptr_t)right % 16 == 0);
+                         ((uintptr_t)left % 16 == 0) && ((uintptr_t)right % 16 == 0) &&
+                         ((uintptr_t)out_codes % 16 == 0) && ((uintptr_t)out_scales % 4 == 0);
     if (allow_mfma && aligned) {
       bool handled = false;
       int st = dispatch_mfma<DT, PACK>(M, N, x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream,

@@ -201,6 +201,32 @@ def test_quantize_matches_sequential_accumulation_oracle(gpu, dtype, mn, monkeyp
     assert int(d.max()) <= 1 and float((d != 0).float().mean()) <= 1e-4 and same >= 0.97
 
 
+@pytest.mark.parametrize("pack", [True, False])
+def test_quantize_misaligned_outputs(gpu, pack, monkeypatch):
+    """Code output not 16-byte aligned (a view 4 bytes / 3 bytes into a buffer):
+    the vector-storing kernels are skipped for the generic one, whose results
+    equal the generic kernel's on aligned outputs; nothing outside the view is
+    written."""
+    case = wl.quant_case("misaligned", 40, 64, 64, torch.float16, 0.9, pack, seed=61)
+    t, f = case.x.shape
+    x, L, R = case.x.to(gpu), case.left.to(gpu), case.right.to(gpu)
+    if pack:
+        big = torch.full((t * f // 8 + 8,), 7, dtype=torch.int32, device=gpu)
+        codes = big[1:1 + t * f // 8].view(t, f // 8)
+    else:
+        big = torch.full((t * f + 16,), 7, dtype=torch.int8, device=gpu)
+        codes = big[3:3 + t * f].view(t, f)
+    _say(f"quantize misaligned codes pack={pack}")
+    q, s = capi.flatquant_quantize(x, L, R, 0.9, pack, out_codes=codes)
+    monkeypatch.setenv("QO_FQ_FORCE_GENERIC", "1")
+    q_ref, s_ref = capi.flatquant_quantize(x, L, R, 0.9, pack)
+    monkeypatch.delenv("QO_FQ_FORCE_GENERIC")
+    torch.cuda.synchronize()
+    assert torch.equal(q, q_ref) and torch.equal(s, s_ref)
+    lo = 1 if pack else 3
+    assert bool((big[:lo] == 7).all()) and bool((big[lo + codes.numel():] == 7).all())
+
+
 def test_quantize_zero_and_constant_tokens(gpu):
     for dtype in (torch.float16, torch.bfloat16):
         for pack in (False, True):
