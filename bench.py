@@ -304,7 +304,7 @@ def cpu_baseline_gemm(torch, budget_s=8.0):
 KERNEL_OF = {
     "quantize_cfg2": "fq_wave_kernel<qo::F16T, 4, 2, true>",
     "quantize_cfg3": "fq_duo_kernel<qo::BF16T, 7, true>",
-    "gemm_cfg4": "gemm_i4_dma<256, 224, 4, 2, 4, false, qo::OutF16>",
+    "gemm_cfg4": "gemm_i4_pp<256, 224, 4, 2, 4, false, qo::OutF16>",
 }
 COPY_PROBE_BYTES = 1 << 30      # float32 negation of 1 GiB: reads and writes exactly this many bytes
 COPY_PROBE_KERNEL = "neg_kernel"

@@ -7,7 +7,7 @@
 // integers is exact, then two separate float32 products, then one rounding.
 //
 // MFMA kernels: gfx950 has no int4 MFMA, so nibbles are widened to int8 and
-// fed to v_mfma_i32_16x16x64_i8. gemm_i4_dma (K % 128 == 0, the main path)
+// fed to v_mfma_i32_16x16x64_i8. gemm_i4_pp (K % 128 == 0, the main path)
 // stages packed words in LDS and widens after the LDS read; gemm_i4_mfma
 // (any K % 8 == 0) widens on the way from registers into LDS. Widening trick: XOR with 0x8 turns the offset code
 // (q + 8) into q's 4-bit two's-complement pattern; placing it in the high half
@@ -298,7 +298,7 @@ gemm_i4_mfma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restri
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined MFMA kernel (gemm_i4_dma): packed words go from global memory to
+// Pipelined MFMA kernel (gemm_i4_pp): packed words go from global memory to
 // LDS by LDS-DMA (global_load_lds_dwordx4, no VGPR staging) through a ring of
 // STAGES buffers, 128 k (16 packed words per row) per stage; nibbles are
 // widened to int8 in registers after the LDS read, so LDS holds and serves
@@ -314,9 +314,11 @@ gemm_i4_mfma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restri
 // B layouts:
 //  * NK (b_stride_p == 1, the W.t() view): B chunks exactly like A's.
 //  * KN (b_stride_n == 1, the reference's [K/8, N]): the DMA copies rows of
-//    packed words (256 columns per 1 KiB DMA) into LDS rows of KN_ROW bytes,
-//    and a lane reads its four words with four ds_read_b32 (rows 4g .. 4g+3,
-//    its column). KN_ROW = 1040 puts the four lane groups on distinct banks.
+//    packed words (256 columns per 1 KiB DMA) into LDS rows of KN_ROW bytes
+//    (1040: the four lane groups' rows start on different banks). A lane needs
+//    words 4g .. 4g+3 of its column, one per row; with the interleaved column
+//    plan (ColPlan) one 16-byte read of a row returns that word for four
+//    adjacent columns, which feed four different accumulator blocks.
 // ---------------------------------------------------------------------------
 
 template <int BM, int BN, bool B_NK>
@@ -371,40 +373,70 @@ __device__ inline void with_scale_dtype(int code, F&& f) {
   else f(std::integral_constant<int, QO_DTYPE_BF16>{});
 }
 
-// Epilogue of a wave's FM x FN blocks of a tile: undo the 256x scale of the
-// widened operands, two float32 products (acc * sa) * sb, one rounding to the
-// output type. acc[i][j][r] holds C[m][n], m = mrow + 16i + li,
-// n = ncol + 16j + 4lg + r (the transposed product), so a lane stores four
-// adjacent outputs; rows and columns past the matrix edge are skipped.
-template <int FM, int FN, class OT>
-__device__ inline void store_c_blocks(const v4i (&acc)[FM][FN], const void* sa, int sad, const void* sb, int sbd,
-                                      typename OT::T* out, int64_t ldc, const typename OT::T* bias, int M, int N,
-                                      int mrow, int ncol, int li, int lg) {
+// Which output columns a wave's FN accumulator blocks hold. A block's 16
+// "rows" in the transposed product are 16 B columns, one per lane li of its
+// operand. Plain (IL false): block j holds columns 16j .. 16j + 15 of the
+// wave's WN. Interleaved (IL true, the [K/8, N] layout, where one LDS read of
+// a packed row returns adjacent columns): the first G4 groups of 64 columns
+// are spread over 4 blocks each, lane li's 16-byte read giving columns
+// 4li .. 4li + 3 to blocks 4q .. 4q + 3; then an optional 32-column group over
+// 2 blocks (8-byte reads); then 16-column blocks as in the plain plan.
+// A lane (li, lg) of block j holds rows r = 0..3, column f (4lg + r) + c of its
+// group (f the interleave, c = the block's place in the group), so it owns FN
+// runs ("chunks") of 4 adjacent columns; chunk u's element e is
+// acc[.][blk(u, e)][reg(u, e)].
+template <int WN, bool IL>
+struct ColPlan {
+  static constexpr int FN = WN / 16;
+  static constexpr int G4 = IL ? WN / 64 : 0;
+  static constexpr int G2 = IL ? (WN % 64) / 32 : 0;
+  static constexpr int J2 = 4 * G4, J1 = 4 * G4 + 2 * G2;   // first block of the 32- and 16-column groups
+  // first column (in the wave's WN) of chunk u for lane group lg
+  __device__ static constexpr int col(int u, int lg) {
+    return u < J2 ? 64 * (u / 4) + 16 * lg + 4 * (u % 4)
+         : u < J1 ? 64 * G4 + 8 * lg + 4 * (u - J2)
+                  : 64 * G4 + 32 * G2 + 16 * (u - J1) + 4 * lg;
+  }
+  __device__ static constexpr int blk(int u, int e) { return u < J2 ? 4 * (u / 4) + e : u < J1 ? J2 + e % 2 : u; }
+  __device__ static constexpr int reg(int u, int e) { return u < J2 ? u % 4 : u < J1 ? 2 * (u - J2) + e / 2 : e; }
+};
+
+// Epilogue of a wave's FM x FN blocks of a tile (float32 outputs): undo the
+// 256x scale of the widened operands, two float32 products (acc * sa) * sb,
+// one rounding to the output type, then the optional bias in the output type,
+// added as the reference's `output + bias.to(dtype)` does (one float32 add of
+// the two output-type values, one rounding back). acc[i][j][r] holds row
+// m = mrow + 16i + li (the transposed product) and the column ColPlan gives; a
+// lane stores runs of four adjacent outputs; rows and columns past the matrix
+// edge are skipped (N % 4 == 0 whenever IL, so a run is all in or all out).
+// The tile's scales and bias are in LDS as float32: ssa = the wave's rows,
+// ssb / sbias = its columns (sbias null: no bias).
+template <int FM, int WN, bool IL, class OT>
+__device__ inline void store_c_lds(const v4i (&acc)[FM][WN / 16], const float* ssa, const float* ssb,
+                                   const float* sbias, typename OT::T* out, int64_t ldc, int M, int N, int mrow,
+                                   int ncol, int li, int lg) {
   using T = typename OT::T;
-  float sav[FM], sbv[FN][4];
-  with_scale_dtype(sad, [&](auto dt) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) sav[i] = scale_at<decltype(dt)::value>(sa, min(mrow + 16 * i + li, M - 1));
-  });
-  with_scale_dtype(sbd, [&](auto dt) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sbv[j][r] = scale_at<decltype(dt)::value>(sb, min(ncol + 16 * j + 4 * lg + r, N - 1));
-  });
+  using CP = ColPlan<WN, IL>;
+  constexpr int FN = CP::FN;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = mrow + 16 * i + li;
+    const float sav = ssa[16 * i + li];
     if (m >= M) continue;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = ncol + 16 * j + 4 * lg;
+    for (int u = 0; u < FN; ++u) {
+      const int c = CP::col(u, lg);
+      const int n = ncol + c;
       if (n >= N) continue;
+      const v4f sbv = *reinterpret_cast<const v4f*>(ssb + c);
       T v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        v[r] = add_bias<OT>(OT::cvt(scale_out(acc[i][j][r] >> 8, sav[i], sbv[j][r])), bias, min(n + r, N - 1));
+      for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(acc[i][CP::blk(u, r)][CP::reg(u, r)] >> 8, sav, sbv[r]));
+      if (sbias) {
+        const v4f bb = *reinterpret_cast<const v4f*>(sbias + c);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = OT::cvt((float)v[r] + bb[r]);
+      }
       T* o = out + (int64_t)m * ldc + n;
       if (n + 3 < N) {
         if constexpr (sizeof(T) == 2) {
@@ -425,158 +457,75 @@ __device__ inline void store_c_blocks(const v4i (&acc)[FM][FN], const void* sa, 
   }
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, bool B_NK, class OT>
-__global__ void __launch_bounds__(64 * WGM * WGN, 1)
-gemm_i4_dma(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
-            const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
-            typename OT::T* __restrict__ out, int64_t ldc, const typename OT::T* __restrict__ bias, int M, int N,
-            int K, int tiles_m) {
-  using S = DmaStage<BM, BN, B_NK>;
-  constexpr int W = WGM * WGN;
-  constexpr int WM = BM / WGM, WN = BN / WGN;
-  constexpr int FM = WM / 16, FN = WN / 16;
-  constexpr int PER = (S::DMA + W - 1) / W;   // DMA instructions per wave per stage
-  static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile");
-  static_assert(STAGES >= 2 && STAGES <= 4, "stages");
-  static_assert(PER * (STAGES - 2) < 64, "vmcnt range");
+// Output value of a 16-bit type as its bit pattern.
+template <class OT>
+__device__ inline uint32_t out_bits(typename OT::T v) {
+  return (uint32_t)(uint16_t)__builtin_bit_cast(uint16_t, v);
+}
 
-  // One LDS object per stage: the compiler can then tell a read of one stage
-  // from the DMA still writing another, and waits only for the right one.
-  __shared__ __align__(16) unsigned char st0[S::BYTES];
-  __shared__ __align__(16) unsigned char st1[S::BYTES];
-  __shared__ __align__(16) unsigned char st2[STAGES > 2 ? S::BYTES : 16];
-  __shared__ __align__(16) unsigned char st3[STAGES > 3 ? S::BYTES : 16];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WGN, wn = wave % WGN;
-  const int li = lane & 15, lg = lane >> 4;
-
-  // XCD-aware tile order (see gemm_i4_mfma).
-  const int nblk = gridDim.x;
-  int pid = blockIdx.x;
-  if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
-  const int tm = pid % tiles_m, tn = pid / tiles_m;
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int nk = K >> 7;                       // stages of 128 k (K % 128 == 0)
-
-  // Source addresses of this wave's DMA instructions at stage 0 (clamped rows
-  // and columns only feed accumulators that are never stored); stage t adds
-  // 16 t words (A, NK) or 16 t rows (KN).
-  const int32_t* src[PER];
-  uint32_t dst[PER];   // wave-uniform LDS offsets inside a stage
-  int64_t step[PER];
+// First half of the staged epilogue: the wave's values (scaled, rounded, bias
+// added as in store_c_lds) written as 8-byte runs into an LDS tile; c_tile
+// points at the wave's first row and column, pitch in bytes.
+template <int FM, int WN, bool IL, class OT>
+__device__ inline void stage_c(const v4i (&acc)[FM][WN / 16], const float* ssa, const float* ssb, const float* sbias,
+                               unsigned char* c_tile, int pitch, int li, int lg) {
+  using T = typename OT::T;
+  using CP = ColPlan<WN, IL>;
+  static_assert(sizeof(T) == 2, "16-bit outputs");
 #pragma unroll
-  for (int t = 0; t < PER; ++t) {
-    int i = __builtin_amdgcn_readfirstlane(wave) + W * t;
-    i = i < S::DMA ? i : S::DMA - 1;           // spare slots repeat the last copy (same bytes, same place)
-    if (i < S::A_DMA) {
-      const int m = min(m0 + 16 * i + li, M - 1);
-      src[t] = a + (int64_t)m * lda + 4 * lg;
-      dst[t] = i * 1024;
-      step[t] = 16;
-    } else if (B_NK) {
-      const int c = i - S::A_DMA;
-      const int n = min(n0 + 16 * c + li, N - 1);
-      src[t] = b + (int64_t)n * ldb + 4 * lg;
-      dst[t] = S::A_BYTES + c * 1024;
-      step[t] = 16;
+  for (int i = 0; i < FM; ++i) {
+    const float sav = ssa[16 * i + li];
+#pragma unroll
+    for (int u = 0; u < CP::FN; ++u) {
+      const int c = CP::col(u, lg);
+      const v4f sbv = *reinterpret_cast<const v4f*>(ssb + c);
+      T v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = OT::cvt(scale_out(acc[i][CP::blk(u, r)][CP::reg(u, r)] >> 8, sav, sbv[r]));
+      if (sbias) {
+        const v4f bb = *reinterpret_cast<const v4f*>(sbias + c);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = OT::cvt((float)v[r] + bb[r]);
+      }
+      *reinterpret_cast<v2i*>(c_tile + (16 * i + li) * pitch + 2 * c) =
+          v2i{(int)(out_bits<OT>(v[0]) | out_bits<OT>(v[1]) << 16), (int)(out_bits<OT>(v[2]) | out_bits<OT>(v[3]) << 16)};
+    }
+  }
+}
+
+// Second half: the workgroup copies the BM x BN tile of 16-bit values from LDS
+// to C in 16-byte pieces, consecutive threads taking consecutive pieces of a
+// row (rows and columns past the matrix edge are skipped; C rows that are not
+// 16-byte aligned take element stores).
+template <int BM, int BN, int THREADS, class OT>
+__device__ inline void copy_out_c(const unsigned char* c_tile, int pitch, typename OT::T* out, int64_t ldc, int M,
+                                  int N, int m0, int n0, int tid) {
+  using T = typename OT::T;
+  constexpr int PPR = BN * 2 / 16;   // 16-byte pieces per row
+  static_assert(BN % 8 == 0 && (BM * PPR) % THREADS == 0, "pieces");
+  const bool vec = ((uintptr_t)out % 16 == 0) && (ldc % 8 == 0);
+#pragma unroll
+  for (int it = 0; it < BM * PPR / THREADS; ++it) {
+    const int p = tid + THREADS * it;
+    const int row = p / PPR, q = p % PPR;
+    const int m = m0 + row, n = n0 + 8 * q;
+    if (m >= M || n >= N) continue;
+    const v4i d = *reinterpret_cast<const v4i*>(c_tile + row * pitch + 16 * q);
+    T* o = out + (int64_t)m * ldc + n;
+    if (vec && n + 7 < N) {
+      *reinterpret_cast<v4i*>(o) = d;
     } else {
-      const int p = i - S::A_DMA;
-      const int n = min(n0 + 4 * lane, N - 4);
-      src[t] = b + (int64_t)p * ldb + n;
-      dst[t] = S::A_BYTES + p * S::KN_ROW;
-      step[t] = 16 * ldb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N) o[e] = __builtin_bit_cast(T, (uint16_t)((uint32_t)d[e / 2] >> (16 * (e % 2))));
     }
   }
-
-  auto stage_ptr = [&](auto buf) -> unsigned char* {
-    constexpr int J = decltype(buf)::value;
-    if constexpr (J == 0) return st0;
-    else if constexpr (J == 1) return st1;
-    else if constexpr (J == 2) return st2;
-    else return st3;
-  };
-  auto issue = [&](int ks, auto buf) {
-    const uint32_t base =
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)stage_ptr(buf);
-#pragma unroll
-    for (int t = 0; t < PER; ++t) dma16(src[t] + ks * step[t], base + dst[t]);
-  };
-
-  v4i acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-
-  auto compute = [&](auto buf) {
-    const unsigned char* base = stage_ptr(buf);
-    v4i ar[FM], br[FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i) ar[i] = *reinterpret_cast<const v4i*>(base + (wm * FM + i) * 1024 + 16 * lane);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      if constexpr (B_NK) {
-        br[j] = *reinterpret_cast<const v4i*>(base + S::A_BYTES + (wn * FN + j) * 1024 + 16 * lane);
-      } else {
-        const unsigned char* col = base + S::A_BYTES + (wn * WN + 16 * j + li) * 4;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) br[j][t] = *reinterpret_cast<const int*>(col + (4 * lg + t) * S::KN_ROW);
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      v4i fa[FM];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) fa[i] = widen_pair(ar[i][2 * h], ar[i][2 * h + 1]);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const v4i fb = widen_pair(br[j][2 * h], br[j][2 * h + 1]);
-        // transposed product: acc[i][j] holds C[16i + lane%16][16j + 4(lane/16) + r]
-#pragma unroll
-        for (int i = 0; i < FM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, fa[i], acc[i][j], 0, 0, 0);
-      }
-    }
-  };
-
-  // Step for stage s held in buffer J = s % STAGES: wait for this wave's DMA
-  // of stage s, barrier (every wave's part has landed and every wave is done
-  // with stage s - 1), refill stage s - 1's buffer with stage s + STAGES - 1,
-  // then the MFMAs of stage s. Past the last stage the refill re-reads stage
-  // nk - 1 into the free buffer, so every step issues the same loads and the
-  // wait count is a constant (a conditional refill makes the compiler wait for
-  // all outstanding loads before the LDS reads that follow it).
-  auto step_stage = [&](int s, auto buf) {
-    constexpr int J = decltype(buf)::value;
-    gemm_wait_vmcnt<PER * (STAGES - 2)>();
-    // lgkmcnt(0): this wave's reads of stage s - 1 have returned before any
-    // wave passes the barrier and refills that buffer
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    issue(min(s + STAGES - 1, nk - 1), std::integral_constant<int, (J + STAGES - 1) % STAGES>{});
-    compute(buf);
-  };
-
-  issue(0, std::integral_constant<int, 0>{});
-  if constexpr (STAGES > 2) issue(min(1, nk - 1), std::integral_constant<int, 1>{});
-  if constexpr (STAGES > 3) issue(min(2, nk - 1), std::integral_constant<int, 2>{});
-  for (int s = 0; s < nk; s += STAGES) {
-    step_stage(s, std::integral_constant<int, 0>{});
-    if (s + 1 < nk) step_stage(s + 1, std::integral_constant<int, 1>{});
-    if constexpr (STAGES > 2)
-      if (s + 2 < nk) step_stage(s + 2, std::integral_constant<int, 2>{});
-    if constexpr (STAGES > 3)
-      if (s + 3 < nk) step_stage(s + 3, std::integral_constant<int, 3>{});
-  }
-  gemm_wait_vmcnt<0>();
-
-  store_c_blocks<FM, FN, OT>(acc, sa, sad, sb, sbd, out, ldc, bias, M, N, m0 + wm * WM, n0 + wn * WN, li, lg);
 }
 
 // ---------------------------------------------------------------------------
-// Register-prefetch variant of gemm_i4_dma (gemm_i4_pp): the same LDS-DMA ring
-// and operand layout, but a stage's packed words are read from LDS into a
-// second register set while the previous stage's MFMAs run, so LDS latency is
-// never waited on between MFMAs. Step s (buffer J = s % STAGES, registers
+// A stage's packed words are read from LDS into a second register set while
+// the previous stage's MFMAs run, so LDS latency is never waited on between
+// MFMAs. Step s (buffer J = s % STAGES, registers
 // P = s % 2, filled during step s - 1):
 //   wait for this wave's DMA of stage s + 1; lgkmcnt(0) + barrier (every
 //   wave's share of stage s + 1 has landed and every wave holds stage s in
@@ -598,10 +547,14 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
   static_assert(STAGES >= 2 && STAGES <= 4 && STAGES % 2 == 0, "stages (even: register sets alternate)");
   static_assert(PER * (STAGES - 1) < 64, "vmcnt range");
 
-  __shared__ __align__(16) unsigned char st0[S::BYTES];
-  __shared__ __align__(16) unsigned char st1[S::BYTES];
-  __shared__ __align__(16) unsigned char st2[STAGES > 2 ? S::BYTES : 16];
-  __shared__ __align__(16) unsigned char st3[STAGES > 3 ? S::BYTES : 16];
+  // The stage ring; after the last stage it holds the output tile on its way
+  // to global memory (16-bit outputs), so it is one object sized for both.
+  constexpr int C_PITCH = BN * 2 + 16;
+  constexpr int RING = STAGES * S::BYTES, CTILE = sizeof(typename OT::T) == 2 ? BM * C_PITCH : 0;
+  __shared__ __align__(16) unsigned char ring[RING > CTILE ? RING : CTILE];
+  __shared__ __align__(16) float s_sa[BM];
+  __shared__ __align__(16) float s_sb[BN];
+  __shared__ __align__(16) float s_bias[BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
@@ -640,15 +593,12 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
       voff[t] = (uint32_t)(p * (int)ldb * 4 + 4 * min(4 * lane, N - 4 - n0));
       dst[t] = S::A_BYTES + p * S::KN_ROW;
     }
+    // wave-uniform: kept in SGPRs (M0 operands), not in VGPRs that compete
+    // with the operands and accumulators
+    dst[t] = __builtin_amdgcn_readfirstlane(dst[t]);
   }
 
-  auto stage_ptr = [&](auto buf) -> unsigned char* {
-    constexpr int J = decltype(buf)::value;
-    if constexpr (J == 0) return st0;
-    else if constexpr (J == 1) return st1;
-    else if constexpr (J == 2) return st2;
-    else return st3;
-  };
+  auto stage_ptr = [&](auto buf) -> unsigned char* { return ring + decltype(buf)::value * S::BYTES; };
   auto issue = [&](int ks, auto buf) {
     const uint32_t base =
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)stage_ptr(buf);
@@ -664,21 +614,46 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-  v4i ar[2][FM], br[2][FN];
+  // B operand words: word(P, j, t) is packed word 4lg + t of block j's column
+  // for this lane. W.t() layout: one 16-byte read per block (br). [K/8, N]
+  // layout, interleaved column plan: per packed row 4lg + t, one 16-byte read
+  // per 64-column group (b4), one 8-byte read for the 32-column group (b2),
+  // one 4-byte read per remaining 16-column block (b1).
+  using CP = ColPlan<WN, !B_NK>;
+  constexpr int N4 = CP::G4 > 0 ? CP::G4 : 1, N1 = FN - CP::J1 > 0 ? FN - CP::J1 : 1;
+  v4i ar[2][FM], br[2][B_NK ? FN : 1];
+  v4i b4[2][4][N4];
+  v2i b2[2][4];
+  int b1[2][4][N1];
+  auto word = [&](auto set, int j, int t) -> int {
+    constexpr int P = decltype(set)::value;
+    if constexpr (B_NK) return br[P][j][t];
+    else if (j < CP::J2) return b4[P][t][j / 4][j % 4];
+    else if (j < CP::J1) return b2[P][t][j - CP::J2];
+    else return b1[P][t][j - CP::J1];
+  };
   auto load_regs = [&](auto buf, auto set) {
     constexpr int P = decltype(set)::value;
     const unsigned char* base = stage_ptr(buf);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
       ar[P][i] = *reinterpret_cast<const v4i*>(base + (wm * FM + i) * 1024 + 16 * lane);
+    if constexpr (B_NK) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      if constexpr (B_NK) {
+      for (int j = 0; j < FN; ++j)
         br[P][j] = *reinterpret_cast<const v4i*>(base + S::A_BYTES + (wn * FN + j) * 1024 + 16 * lane);
-      } else {
-        const unsigned char* col = base + S::A_BYTES + (wn * WN + 16 * j + li) * 4;
+    } else {
+      const unsigned char* cols = base + S::A_BYTES + wn * WN * 4;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) br[P][j][t] = *reinterpret_cast<const int*>(col + (4 * lg + t) * S::KN_ROW);
+      for (int t = 0; t < 4; ++t) {
+        const unsigned char* row = cols + (4 * lg + t) * S::KN_ROW;
+#pragma unroll
+        for (int q = 0; q < CP::G4; ++q) b4[P][t][q] = *reinterpret_cast<const v4i*>(row + 256 * q + 16 * li);
+        if constexpr (CP::G2 > 0) b2[P][t] = *reinterpret_cast<const v2i*>(row + 256 * CP::G4 + 8 * li);
+#pragma unroll
+        for (int j = CP::J1; j < FN; ++j)
+          b1[P][t][j - CP::J1] = *reinterpret_cast<const int*>(row + 256 * CP::G4 + 128 * CP::G2 +
+                                                               64 * (j - CP::J1) + 4 * li);
       }
     }
   };
@@ -691,7 +666,7 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
       for (int i = 0; i < FM; ++i) fa[i] = widen_pair(ar[P][i][2 * h], ar[P][i][2 * h + 1]);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const v4i fb = widen_pair(br[P][j][2 * h], br[P][j][2 * h + 1]);
+        const v4i fb = widen_pair(word(set, j, 2 * h), word(set, j, 2 * h + 1));
 #pragma unroll
         for (int i = 0; i < FM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, fa[i], acc[i][j], 0, 0, 0);
       }
@@ -715,12 +690,27 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
     compute(set);
   };
 
+  // The tile's scales (and bias) as float32 in LDS for the epilogue: one load
+  // per thread, issued before the first stages' copies so that its latency
+  // overlaps theirs.
+  static_assert(BM <= 256 && BN <= 64 * W - 256, "one scale per thread");
+  float sv = 0.f, bv = 0.f;
+  if (tid < BM) sv = load_scale(sa, sad, min(m0 + tid, M - 1));
+  else if (tid - 256 < BN) {
+    sv = load_scale(sb, sbd, min(n0 + tid - 256, N - 1));
+    if (bias) bv = (float)bias[min(n0 + tid - 256, N - 1)];
+  }
   issue(0, std::integral_constant<int, 0>{});
   issue(min(1, nk - 1), std::integral_constant<int, 1>{});
   if constexpr (STAGES > 2) issue(min(2, nk - 1), std::integral_constant<int, 2>{});
   if constexpr (STAGES > 3) issue(min(3, nk - 1), std::integral_constant<int, 3>{});
   gemm_wait_vmcnt<PER * (STAGES - 1)>();
-  asm volatile("s_barrier" ::: "memory");
+  if (tid < BM) s_sa[tid] = sv;
+  else if (tid - 256 < BN) {
+    s_sb[tid - 256] = sv;
+    s_bias[tid - 256] = bv;
+  }
+  lds_barrier();
   load_regs(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
   for (int s = 0; s < nk; s += STAGES) {
     step_stage(s, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
@@ -732,7 +722,20 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
   }
   gemm_wait_vmcnt<0>();
 
-  store_c_blocks<FM, FN, OT>(acc, sa, sad, sb, sbd, out, ldc, bias, M, N, m0 + wm * WM, n0 + wn * WN, li, lg);
+  const float* sbias = bias ? s_bias + wn * WN : nullptr;
+  if constexpr (CTILE > 0) {
+    // 16-bit outputs: the tile goes through LDS so that each store
+    // instruction writes whole 16-byte pieces of a few rows (the store
+    // instruction count, not the bytes, bounds the epilogue).
+    lds_barrier();   // every wave is done with the ring (its copies were waited above)
+    stage_c<FM, WN, !B_NK, OT>(acc, s_sa + wm * WM, s_sb + wn * WN, sbias, ring + wm * WM * C_PITCH + wn * WN * 2,
+                               C_PITCH, li, lg);
+    lds_barrier();
+    copy_out_c<BM, BN, 64 * W, OT>(ring, C_PITCH, out, ldc, M, N, m0, n0, tid);
+  } else {
+    store_c_lds<FM, WN, !B_NK, OT>(acc, s_sa + wm * WM, s_sb + wn * WN, sbias, out, ldc, M, N, m0 + wm * WM,
+                                   n0 + wn * WN, li, lg);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -889,20 +892,14 @@ static void launch_mfma(const int32_t* a, int64_t lda, const int32_t* b, int64_t
                      tiles_n);
 }
 
-// Launch of the pipelined kernels: 4 x 2 waves, four-stage ring. The W.t()
-// layout (B_NK) takes the register-prefetch kernel gemm_i4_pp; the row-major
-// [K/8, N] layout keeps gemm_i4_dma, whose four 4-byte column reads per
-// operand would not fit a second register set within 256 VGPRs.
+// Launch of the pipelined kernel: 4 x 2 waves, four-stage ring, either B layout.
 template <int BM, int BN, bool B_NK, class OT>
 static void launch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
                        const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K, hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  if constexpr (B_NK)
-    hipLaunchKernelGGL((gemm_i4_pp<BM, BN, 4, 2, 4, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a,
-                       lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, reinterpret_cast<const typename OT::T*>(bias), M, N, K, tiles_m);
-  else
-    hipLaunchKernelGGL((gemm_i4_dma<BM, BN, 4, 2, 4, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a,
-                       lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, reinterpret_cast<const typename OT::T*>(bias), M, N, K, tiles_m);
+  hipLaunchKernelGGL((gemm_i4_pp<BM, BN, 4, 2, 4, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a, lda,
+                     b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc,
+                     reinterpret_cast<const typename OT::T*>(bias), M, N, K, tiles_m);
 }
 
 // Fraction of the machine's workgroup slots doing useful output in a launch
