@@ -863,6 +863,155 @@ gemm_i4_skinny(const int32_t* __restrict__ a, int64_t lda, const int32_t* __rest
 }
 
 // ---------------------------------------------------------------------------
+// Skinny kernel for the W.t() layout (gemm_i4_skinny_nk), the decode GEMM of
+// the linear layer. Same split as gemm_i4_skinny (16 output columns and all M
+// rows per workgroup, exact int32 sums of per-wave partials through LDS), but
+// A and B reach LDS by LDS-DMA in "chunks" of CB contiguous bytes of every
+// row (the 16 B rows = columns n0 .. n0 + 15, then the 16 MT rows of A): each
+// DMA instruction reads 1 KiB of one or two rows. Measured at 16 x 4096 x
+// 14336, the same bytes read as 16 rows x 64 B per instruction (one MFMA
+// operand straight into registers) take half as long again.
+// Chunk c holds stages c SPC .. c SPC + SPC - 1 (stage = 64 B = 128 k per row);
+// wave w multiplies SPW of them. LDS slot of 16-byte piece p of row r is
+// p ^ (r % 16), so the 16 rows of an operand read sit on distinct banks (the
+// DMA's lane -> slot placement is fixed, its source addresses are permuted).
+// Chunks go through a ring of RING buffers behind one barrier each, as the
+// tiled kernels' stages do.
+// ---------------------------------------------------------------------------
+template <int MT>
+struct SkinnyNkCfg {
+  static constexpr int CB = MT == 1 ? 1024 : 512;            // bytes per row per chunk
+  static constexpr int SPC = CB / 64, SPW = SPC / 8;         // stages per chunk, per wave
+  static constexpr int ROWS = 16 + 16 * MT;
+  static constexpr int BUF = ROWS * CB;
+  static constexpr int RING = 4 * BUF <= 150 * 1024 ? 4 : 3;
+  static constexpr int NI = BUF / 1024;                      // DMA instructions per chunk
+  static constexpr int D = (NI + 7) / 8;                     // ... per wave
+  static_assert(SPW >= 1 && D * (RING - 2) < 64, "chunk shape");
+};
+
+template <int MT, class OT>
+__global__ void __launch_bounds__(512)
+gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
+                  const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
+                  typename OT::T* __restrict__ out, int64_t ldc, const typename OT::T* __restrict__ bias, int M,
+                  int N, int K) {
+  using C = SkinnyNkCfg<MT>;
+  __shared__ __align__(16) unsigned char ring[C::RING * C::BUF];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int nk = K >> 7;                        // stages
+  const int rowbytes = K >> 1;                  // bytes of a packed row
+  const int nch = (rowbytes + C::CB - 1) / C::CB;
+
+  // DMA instruction t of this wave: SGPR base (its first row), the lane's
+  // offset to its row (the second row for CB = 512) and to its swizzled piece,
+  // and the LDS destination.
+  const char* rbase[C::D];
+  uint32_t rdiff[C::D], poff[C::D], ldst[C::D];
+  auto row_ptr = [&](int r) -> const char* {
+    return r < 16 ? reinterpret_cast<const char*>(b + (int64_t)min(n0 + r, N - 1) * ldb)
+                  : reinterpret_cast<const char*>(a + (int64_t)min(r - 16, M - 1) * lda);
+  };
+#pragma unroll
+  for (int t = 0; t < C::D; ++t) {
+    int i = __builtin_amdgcn_readfirstlane(wave) + 8 * t;
+    i = i < C::NI ? i : C::NI - 1;              // spare slots repeat the last copy
+    constexpr int RPI = 1024 / C::CB;           // rows per instruction
+    const int r0 = RPI * i;
+    const int r = r0 + (RPI == 2 ? lane >> 5 : 0);
+    const int q = RPI == 2 ? lane & 31 : lane;  // LDS slot in the row
+    rbase[t] = row_ptr(r0);
+    rdiff[t] = (uint32_t)(row_ptr(r) - row_ptr(r0));   // 0 or one row stride (rows clamp monotonically)
+    poff[t] = 16 * (q ^ (r & 15));
+    ldst[t] = __builtin_amdgcn_readfirstlane(i * 1024);
+  }
+  auto issue = [&](int c, int buf) {
+    const uint32_t base = lds_addr(ring) + buf * C::BUF;
+    const uint32_t coff = c * C::CB;
+#pragma unroll
+    for (int t = 0; t < C::D; ++t)   // pieces past the row's end re-read its last piece (never multiplied)
+      dma16_s(rdiff[t] + min(coff + poff[t], (uint32_t)rowbytes - 16), rbase[t], base + ldst[t]);
+  };
+
+  v4i acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+
+  auto compute = [&](int c, int buf) {
+    const unsigned char* base = ring + buf * C::BUF;
+#pragma unroll
+    for (int u = 0; u < C::SPW; ++u) {
+      const int ls = wave * C::SPW + u;         // stage within the chunk
+      if (c * C::SPC + ls >= nk) break;
+      const int slot = (4 * ls + lg) ^ li;
+      const v4i bw = *reinterpret_cast<const v4i*>(base + li * C::CB + 16 * slot);
+      v4i aw[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        aw[mt] = *reinterpret_cast<const v4i*>(base + (16 + 16 * mt + li) * C::CB + 16 * slot);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const v4i fb = widen_pair(bw[2 * h], bw[2 * h + 1]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, widen_pair(aw[mt][2 * h], aw[mt][2 * h + 1]), acc[mt],
+                                                          0, 0, 0);
+      }
+    }
+  };
+
+  for (int c = 0; c < C::RING - 1; ++c) issue(min(c, nch - 1), c);
+  for (int c = 0; c < nch; ++c) {
+    gemm_wait_vmcnt<C::D * (C::RING - 2)>();
+    lds_barrier();   // chunk c has landed for every wave; every wave is done with chunk c - 1's buffer
+    issue(min(c + C::RING - 1, nch - 1), (c + C::RING - 1) % C::RING);
+    compute(c, c % C::RING);
+  }
+  gemm_wait_vmcnt<0>();
+  lds_barrier();
+
+  // Partials of the 8 waves, summed exactly by waves 0 .. MT-1 (one 16-row
+  // block each), then (float(acc) * sa) * sb, one rounding, optional bias.
+  v4i* part = reinterpret_cast<v4i*>(ring);     // [8][MT][64]
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) part[(wave * MT + mt) * 64 + lane] = acc[mt];
+  __syncthreads();
+  if (wave >= MT) return;
+  const int mt = wave;
+  v4i sum = part[mt * 64 + lane];
+#pragma unroll
+  for (int w = 1; w < 8; ++w) sum += part[(w * MT + mt) * 64 + lane];
+  const int m = 16 * mt + li;
+  const int nc = n0 + 4 * lg;
+  if (m >= M || nc >= N) return;
+  using T = typename OT::T;
+  const float sam = load_scale(sa, sad, m);
+  T v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    v[r] = add_bias<OT>(OT::cvt(scale_out(sum[r] >> 8, sam, load_scale(sb, sbd, min(nc + r, N - 1)))), bias,
+                        min(nc + r, N - 1));
+  T* o = out + (int64_t)m * ldc + nc;
+  if (nc + 3 < N) {
+    if constexpr (sizeof(T) == 2) {
+      typedef short v4s __attribute__((ext_vector_type(4)));
+      v4s pk;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
+      *reinterpret_cast<v4s*>(o) = pk;
+    } else {
+      *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (nc + r < N) o[r] = v[r];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host dispatch.
 // ---------------------------------------------------------------------------
 
@@ -948,8 +1097,13 @@ static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64
   const dim3 grid((unsigned)((N + 15) / 16));
   using T = typename OT::T;
   auto go = [&](auto mt, auto nk_layout) {
-    hipLaunchKernelGGL((gemm_i4_skinny<decltype(mt)::value, decltype(nk_layout)::value, OT>), grid, dim3(512), 0,
-                       stream, a, lda, b, ldb, sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
+    if constexpr (decltype(nk_layout)::value)
+      hipLaunchKernelGGL((gemm_i4_skinny_nk<decltype(mt)::value, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb,
+                         sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
+    else
+      hipLaunchKernelGGL((gemm_i4_skinny<decltype(mt)::value, false, OT>), grid, dim3(512), 0, stream, a, lda, b,
+                         ldb, sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N,
+                         K);
   };
   auto by_layout = [&](auto mt) {
     if (b_nk) go(mt, std::true_type{});
