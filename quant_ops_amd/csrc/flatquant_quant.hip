@@ -646,6 +646,24 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 // routes clip <= 0 elsewhere.
 // ---------------------------------------------------------------------------
 
+// LDS transpose read of 16-bit elements (gfx950 ds_read_b64_tr_b16): within
+// each 16-lane group, lane l supplies the address of 4 consecutive elements
+// (8-byte aligned), forming row l of a 16 x 4 matrix A; lane i receives
+// A[i/4][i%4], A[4 + i/4][i%4], A[8 + i/4][i%4], A[12 + i/4][i%4] — that is,
+// A[4e + i/4][i%4] for e = 0..3 (checked on the device).
+typedef short v4s16 __attribute__((ext_vector_type(4)));
+__device__ inline v4s16 lds_tr16(const void* p) {
+  typedef __attribute__((address_space(3))) v4s16* lds_v4s16;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s16)(__attribute__((address_space(3))) const void*)p);
+}
+// Two 4-element reads as one 8-element MFMA operand (elements 0..3, 4..7).
+template <class V>
+__device__ inline V join_tr16(v4s16 lo, v4s16 hi) {
+  typedef short v8s16 __attribute__((ext_vector_type(8)));
+  const v8s16 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(V, w);
+}
+
 template <class DT>
 struct DBits;
 template <>
@@ -1088,38 +1106,37 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     }
     lds_barrier();
   }
+  // Both gathers below read 4 consecutive rows of one column per lane with
+  // the LDS transpose read (lds_tr16): lane l of a 16-lane group supplies the
+  // address of row k0 + l/4, columns C(l%4) .. C(l%4) + 3, and receives rows
+  // k0 .. k0 + 3 of column C(l/4) + l%4.
   // R fragments of this wave's columns: rf[q][h][ks][j] = R[32ks + 8lg + j][n],
-  // n = 64c + 16(li/4) + 8q + 4h + li%4.
+  // n = 64c + 16(li/4) + 8q + 4h + li%4, i.e. C(x) = 64c + 16x + 8q + 4h.
   V rf[2][2][KS1];
   {
     const T* rs = reinterpret_cast<const T*>(stage);
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int n = 64 * c + 16 * (li >> 2) + 8 * q + 4 * h + (li & 3);
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int ks = 0; ks < KS1; ++ks)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) rf[q][h][ks][j] = rs[(32 * ks + 8 * lg + j) * N + n];
-      }
+        for (int ks = 0; ks < KS1; ++ks) {
+          const T* at = rs + (32 * ks + 8 * lg + (li >> 2)) * N + 64 * c + 16 * (li & 3) + 8 * q + 4 * h;
+          rf[q][h][ks] = join_tr16<V>(lds_tr16(at), lds_tr16(at + 4 * N));
+        }
   }
   // L fragments (16 bytes per lane and slab): slab (mb, s), lane l, element j
-  // holds L[32s + 16(j/4) + 4(l/16) + j%4][16mb + l%16]; in the zero-padded
-  // tail slab (s = KS2, M / 16 odd) elements 4..7 are zero.
+  // holds L[32s + 16(j/4) + 4(l/16) + j%4][16mb + l%16] (C(x) = 16mb + 4x); in
+  // the zero-padded tail slab (s = KS2, M / 16 odd) elements 4..7 are zero.
   {
     const T* ls = reinterpret_cast<const T*>(stage + N * N * 2);
 #pragma unroll 1
     for (int fr = wave; fr < MB * S::KSL; fr += 2 * SLOTS) {
       const int mb = fr / S::KSL, sl = fr % S::KSL;
-      const int m = 16 * mb + li;
-      V v;
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int mp = 32 * sl + 16 * (jj >> 2) + 4 * lg + (jj & 3);
-        v[jj] = (sl == KS2 && jj >= 4) ? __builtin_bit_cast(T, (short)0) : ls[mp * M + m];
-      }
-      *reinterpret_cast<V*>(lfs + fr * 1024 + 16 * lane) = v;
+      const T* at = ls + (32 * sl + 4 * lg + (li >> 2)) * M + 16 * mb + 4 * (li & 3);
+      const v4s16 lo = lds_tr16(at);
+      const v4s16 hi = sl == KS2 ? v4s16{0, 0, 0, 0} : lds_tr16(at + 16 * M);
+      *reinterpret_cast<V*>(lfs + fr * 1024 + 16 * lane) = join_tr16<V>(lo, hi);
     }
   }
   lds_barrier();   // R in registers, L fragments written: the staging space is free
