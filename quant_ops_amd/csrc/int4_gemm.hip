@@ -563,7 +563,16 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
   const int nblk = gridDim.x;
   int pid = blockIdx.x;
   if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
-  const int tm = pid % tiles_m, tn = pid / tiles_m;
+  // Grouped tile order: groups of 4 row tiles x every column tile, so the
+  // workgroups an XCD runs at once cover a compact block of C and share its
+  // A and B tiles in that XCD's L2 (at 4096 x 14336: 4 row tiles and 8 column
+  // tiles instead of all 16 row tiles and 2 column tiles; 1-5 % faster at the
+  // benched shapes).
+  constexpr int GM = 4;
+  const int tiles_n = (N + BN - 1) / BN;
+  const int g = pid / (GM * tiles_n), w = pid % (GM * tiles_n);
+  const int gm = min(GM, tiles_m - g * GM);
+  const int tm = g * GM + w % gm, tn = w / gm;
   const int m0 = tm * BM, n0 = tn * BN;
   const int nk = K >> 7;
 
