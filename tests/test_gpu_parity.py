@@ -410,6 +410,34 @@ def test_gemm_skinny_bit_exact(gpu, m, n, k, bview, monkeypatch):
     assert torch.equal(out, out_tiled)
 
 
+@pytest.mark.parametrize("bview", [False, True])
+def test_gemm_tiny_and_special_row_scales(gpu, bview):
+    """Row scales that are tiny (below 2^-118), subnormal, zero, negative,
+    inf and NaN, in some 16-row blocks and not others: every output equals the
+    reference's (acc * sa) * sb, NaN where it is NaN (bf16 output keeps the
+    float32 range, so tiny products stay visible)."""
+    m, n, k = 300, 260, 1024
+    case = wl.gemm_case(m, n, k, seed=31, b_transposed_view=bview)
+    sa = case.scale_a.clone()
+    sa[5] = 1e-37               # normal, below 2^-118
+    sa[40] = 3e-39              # subnormal
+    sa[41] = 0.0
+    sa[77] = -2.0 ** -118       # exactly at the bound
+    sa[130] = -0.05
+    sa[200] = float("inf")
+    sa[201] = float("nan")
+    sa[299] = 2.0 ** -120
+    sb = case.scale_b.clone() * 1e3
+    _say(f"gemm special row scales bview={bview}")
+    out = capi.int4_gemm(case.a.to(gpu), case.b.to(gpu), sa.to(gpu), sb.to(gpu), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    ref = oi4.int4_matmul_pytorch(case.a, case.b, sa, sb, out_dtype=torch.bfloat16)
+    o, r = out.cpu().view(torch.int16), ref.view(torch.int16)
+    nan_o, nan_r = torch.isnan(out.cpu()), torch.isnan(ref)
+    assert torch.equal(nan_o, nan_r)
+    assert torch.equal(o[~nan_o], r[~nan_r])
+
+
 @pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
 def test_gemm_scale_and_out_dtypes(gpu, sdt, odt):
