@@ -438,6 +438,29 @@ def test_gemm_tiny_and_special_row_scales(gpu, bview):
     assert torch.equal(o[~nan_o], r[~nan_r])
 
 
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("m,n,k,bview", [(300, 260, 1024, False), (300, 260, 1024, True), (16, 300, 1024, True),
+                                         (16, 300, 1024, False)])
+def test_gemm_strided_output_rows(gpu, odt, m, n, k, bview):
+    """Output rows inside a wider buffer, starting 4 elements in, row stride
+    n + 16 (for 16-bit outputs: 8-byte but not 16-byte aligned rows, which
+    the tiled kernel's 16-byte row pieces must not assume); with a bias. Nothing
+    outside the view is written."""
+    case = wl.gemm_case(m, n, k, seed=m + n, b_transposed_view=bview)
+    g = torch.Generator().manual_seed(n)
+    bias = (torch.randn(n, generator=g) * 2).to(odt)
+    big = torch.full((m, n + 16), 7.0, dtype=odt, device=gpu)
+    view = big[:, 4:4 + n]
+    _say(f"gemm strided out {m}x{n}x{k} bview={bview} {odt}")
+    capi.int4_gemm(case.a.to(gpu), case.b.to(gpu), case.scale_a.to(gpu), case.scale_b.to(gpu), out=view,
+                   bias=bias.to(gpu))
+    torch.cuda.synchronize()
+    ref = oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b, out_dtype=odt) + bias
+    b = big.cpu()
+    assert torch.equal(b[:, 4:4 + n], ref)
+    assert bool((b[:, :4] == 7.0).all()) and bool((b[:, 4 + n:] == 7.0).all())
+
+
 @pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
 def test_gemm_scale_and_out_dtypes(gpu, sdt, odt):
