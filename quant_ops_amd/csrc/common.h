@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "quant_ops_hip.h"
 
 namespace qo {
@@ -138,6 +140,23 @@ __device__ inline void dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
 template <class P>
 __device__ inline uint32_t lds_addr(P* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// Compute units of the current device (host side), for grid sizing; queried
+// once per device and cached (thread-safe). 256 (MI355X) if the query fails.
+inline int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < kMaxDevices) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (dev < kMaxDevices) cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
 }
 
 // Workgroup barriers without the release/acquire fences of __syncthreads():

@@ -1295,14 +1295,6 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
 
-static int device_cu_count() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return 256;
-  return cus;
-}
-
 template <class DT, int MB, int NP, bool PACK>
 static int launch_mfma(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right,
                        float clip, void* out_codes, float* out_scales, hipStream_t stream) {

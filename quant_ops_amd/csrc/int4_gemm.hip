@@ -1070,22 +1070,11 @@ static double tile_efficiency(int64_t M, int64_t N, int BM, int BN, int cus) {
 }
 
 
-static int gemm_cu_count() {
-  static int cached = 0;
-  if (cached) return cached;
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) == hipSuccess &&
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-    cached = cus;
-  else
-    cached = 256;
-  return cached;
-}
 
 template <bool B_NK, class OT>
 static void dispatch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
                          const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K, hipStream_t stream) {
-  const int cus = gemm_cu_count();
+  const int cus = device_cu_count();
   if (tile_efficiency(M, N, 256, 224, cus) > tile_efficiency(M, N, 256, 256, cus))
     launch_dma<256, 224, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
   else
