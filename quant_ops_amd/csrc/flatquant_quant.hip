@@ -714,11 +714,6 @@ __device__ inline void fq_wave_load_x(const typename DT::T* __restrict__ xt,
       xf[rb][ks] = *reinterpret_cast<const typename MfmaOps<DT>::V*>(xt + (16 * rb + li) * N + 32 * ks + 8 * lg);
 }
 
-// Transform fragments: R's rf[q][h][ks] at index (2q + h) KS1 + ks, then L's
-// lf[mb][s] at 2 NQ KS1 + mb KS2 + s; one 1 KiB fragment per index (16 bytes
-// per lane). A build job is one pair of row tiles and the two fragments its
-// selection products give: R job (q, ks) -> rf[q][0..1][ks], L job (s, p) ->
-// lf[2p..2p+1][s].
 // Store N adjacent 32-bit words (N = 1, 2 or 4) with one instruction.
 template <int NW_>
 __device__ inline void store_words(int32_t* dst, const uint32_t (&w)[NW_]) {
@@ -745,6 +740,11 @@ __device__ inline void fq_wave_store_codes(int32_t* orow, const uint32_t (&yp)[M
   }
 }
 
+// Transform fragments of the wave kernel in LDS: R's rf[q][h][ks] at index
+// (2q + h) KS1 + ks, then L's lf[mb][s] at 2 NQ KS1 + mb KS2 + s; one 1 KiB
+// fragment per index (16 bytes per lane). A build job is one pair of row tiles
+// and the two fragments its selection products give: R job (q, ks) ->
+// rf[q][0..1][ks], L job (s, p) -> lf[2p..2p+1][s].
 template <int MB, int NQ>
 struct WaveFrags {
   static constexpr int KS1 = NQ, KS2 = MB / 2;
