@@ -82,29 +82,66 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
   T* zs = xs + F;
   __shared__ float red_hi[4], red_lo[4], s_scale;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  auto r_at = [&](int i) { return DT::to_f(right[i]); };
+  auto l_at = [&](int i) { return DT::to_f(left[i]); };
 
   for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
     const T* xt = x + t * x_ld;
     for (int f = tid; f < F; f += 256) xs[f] = xt[f];
     __syncthreads();
+    // Both contractions in 4 x 4 output tiles per thread (rows m0.., columns
+    // n0..; consecutive threads take consecutive column groups, so the global
+    // reads of R and L coalesce), accumulated in float32 over k in order.
+    const int nb = (N + 3) >> 2, tiles = ((M + 3) >> 2) * nb;
     // Z = rnd_D(X R): Z[m][n] = sum_k X[m][k] R[k][n]
-    for (int f = tid; f < F; f += 256) {
-      const int m = f / N, n = f - m * N;
-      float acc = 0.f;
-      for (int k = 0; k < N; ++k) acc = fmaf(DT::to_f(xs[m * N + k]), DT::to_f(right[k * N + n]), acc);
-      zs[f] = DT::from_f(acc);
+    for (int tl = tid; tl < tiles; tl += 256) {
+      const int m0 = tl / nb * 4, n0 = (tl % nb) * 4;
+      float acc[4][4] = {};
+      for (int k = 0; k < N; ++k) {
+        float xv[4], rv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xv[i] = m0 + i < M ? DT::to_f(xs[(m0 + i) * N + k]) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rv[j] = n0 + j < N ? r_at(k * N + n0 + j) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], rv[j], acc[i][j]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (m0 + i < M && n0 + j < N) zs[(m0 + i) * N + n0 + j] = DT::from_f(acc[i][j]);
     }
     __syncthreads();
     // Y = rnd_D(L^T Z): Y[m][n] = sum_k L[k][m] Z[k][n]
     float hi = -INFINITY, lo = INFINITY;
-    for (int f = tid; f < F; f += 256) {
-      const int m = f / N, n = f - m * N;
-      float acc = 0.f;
-      for (int k = 0; k < M; ++k) acc = fmaf(DT::to_f(left[k * M + m]), DT::to_f(zs[k * N + n]), acc);
-      const T y = DT::from_f(acc);
-      xs[f] = y;
-      hi = fmaxf(hi, DT::to_f(y));
-      lo = fminf(lo, DT::to_f(y));
+    for (int tl = tid; tl < tiles; tl += 256) {
+      const int m0 = tl / nb * 4, n0 = (tl % nb) * 4;
+      float acc[4][4] = {};
+      for (int k = 0; k < M; ++k) {
+        float lv[4], zv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lv[i] = m0 + i < M ? l_at(k * M + m0 + i) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) zv[j] = n0 + j < N ? DT::to_f(zs[k * N + n0 + j]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(lv[i], zv[j], acc[i][j]);
+      }
+      // Y goes into X's buffer: X was last read before the barrier above
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (m0 + i < M && n0 + j < N) {
+            const T y = DT::from_f(acc[i][j]);
+            xs[(m0 + i) * N + n0 + j] = y;
+            hi = fmaxf(hi, DT::to_f(y));
+            lo = fminf(lo, DT::to_f(y));
+          }
     }
     hi = wave_max(hi);
     lo = wave_min(lo);
@@ -1391,7 +1428,7 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE(8, 4)   // 128 x 128  (hidden 16384)
   QO_FQ_CASE(2, 1)   // 32 x 32    (hidden 1024)
   QO_FQ_CASE(3, 2)   // 48 x 64    (hidden 3072)
-  QO_FQ_CASE(5, 2)   // 80 x 64    (hidden 5120)
+  QO_FQ_CASE(5, 2)   // 80 x 64    (get_decompose_dim(5120) is 64 x 80, which takes the generic kernel)
   QO_FQ_CASE(6, 4)   // 96 x 128   (hidden 12288)
 #undef QO_FQ_CASE
   *handled = false;
