@@ -7,7 +7,7 @@
 // points of its PyTorch fallback (flatquant/ops.py:99-130).
 //
 // Two kernels:
-//  * fq_mfma_kernel   — D in {fp16, bf16}, M % 16 == 0 (M <= 128), N in {32, 64, 128}.
+//  * fq_mfma_kernel   — D in {fp16, bf16}, M % 16 == 0 (M <= 128), N = 32 NP (listed shapes).
 //                       Both contractions on v_mfma_f32_16x16x32_{f16,bf16}; X is
 //                       streamed into LDS by LDS-DMA (global_load_lds_dwordx4)
 //                       one token group ahead; L is resident in LDS, R in VGPRs.
@@ -1430,6 +1430,11 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE(3, 2)   // 48 x 64    (hidden 3072)
   QO_FQ_CASE(5, 2)   // 80 x 64    (get_decompose_dim(5120) is 64 x 80, which takes the generic kernel)
   QO_FQ_CASE(6, 4)   // 96 x 128   (hidden 12288)
+  QO_FQ_CASE(4, 3)   // 64 x 96    (hidden 6144)
+  QO_FQ_CASE(5, 4)   // 80 x 128   (hidden 10240)
+  QO_FQ_CASE(8, 5)   // 128 x 160  (hidden 20480)
+  QO_FQ_CASE(8, 6)   // 128 x 192  (hidden 24576)
+  QO_FQ_CASE(8, 7)   // 128 x 224  (hidden 28672)
 #undef QO_FQ_CASE
   *handled = false;
   return QO_OK;

@@ -114,6 +114,12 @@ SHAPES = [
     (2, 8, 8, torch.float16, 0.9, False),        # generic kernel
     (5, 12, 20, torch.float32, 1.0, False),      # generic kernel, fp32
     (4, 64, 64, torch.float32, 0.9, True),
+    (9, 64, 96, torch.float16, 0.9, True),       # three-wave MFMA groups (N = 96, hidden 6144)
+    (5, 80, 128, torch.bfloat16, 1.0, True),     # MFMA kernel, odd M / 16 (hidden 10240)
+    (4, 128, 160, torch.float16, 1.0, False),    # N = 160 (hidden 20480)
+    (2, 128, 192, torch.bfloat16, 0.9, True),    # N = 192 (hidden 24576)
+    (3, 128, 224, torch.bfloat16, 0.9, True),    # N = 224 (hidden 28672)
+    (6, 64, 80, torch.float16, 0.9, True),       # generic kernel (hidden 5120)
 ]
 
 
@@ -127,7 +133,7 @@ def test_quantize_shapes(gpu, t, m, n, dtype, clip, pack):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("mn", [(64, 64), (112, 128)])
+@pytest.mark.parametrize("mn", [(64, 64), (112, 128), (64, 96), (128, 224)])
 def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
     m, n = mn
     case = wl.quant_case("xcheck", 37, m, n, dtype, 0.9, True, seed=5, outlier_frac=0.005, outlier_scale=30.0)
