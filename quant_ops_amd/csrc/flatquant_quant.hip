@@ -382,11 +382,16 @@ struct FqEpi<BF16T> {
   __device__ static inline uint32_t amax_bits(const Amax& a) { return max(a.m & 0xFFFFu, a.m >> 16); }
 };
 
-template <int MB, int NP>
+// NV: the row width in memory; N = 32 NP is the width computed, and columns
+// NV .. N - 1 are zero padding (X's padded k zeroed in registers, R's padded
+// rows and columns zero, padded codes not stored; their Y values are 0, which
+// leaves max |Y| unchanged).
+template <int MB, int NP, int NV = 32 * NP>
 struct FqShape {
   static constexpr int M = 16 * MB;
   static constexpr int N = 32 * NP;
-  static constexpr int F = M * N;
+  static constexpr int F = M * NV;
+  static_assert(NV % 8 == 0 && NV > 32 * (NP - 1) && NV <= N, "valid width");
   static constexpr int KS1 = NP;             // 32-deep slabs of the first product (k = n')
   static constexpr int KS2 = MB / 2;         // full 32-deep slabs of the second product (k = m')
   static constexpr bool TAIL = (MB & 1) != 0; // plus one 16-deep slab when M is an odd multiple of 16
@@ -414,18 +419,20 @@ __device__ inline void wait_vmcnt() {
 
 // One token group (this wave's token slot and pair) from an X stage in LDS:
 // both products, the per-token scale and the codes.
-template <class DT, int MB, int NP, bool PACK>
+template <class DT, int MB, int NP, bool PACK, int NV>
 __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FqShape<MB, NP>::KS2 + 1],
     const typename MfmaOps<DT>::V (&rf)[2][FqShape<MB, NP>::KS1], float (*red)[NP][2], int64_t t,
     int64_t tokens, float clip, void* __restrict__ out_codes, float* __restrict__ out_scales, int lane,
     int tau, int q) {
-  using S = FqShape<MB, NP>;
+  using S = FqShape<MB, NP, NV>;
   using T = typename DT::T;
   using Ops = MfmaOps<DT>;
   using V = typename Ops::V;
-  constexpr int N = S::N, F = S::F, KS1 = S::KS1, KS2 = S::KS2;
+  constexpr int F = S::F, KS1 = S::KS1, KS2 = S::KS2;
   const int li = lane & 15, lg = lane >> 4;
+  // this lane's 8 columns of its pair: stored only inside the valid width
+  const bool col_ok = 32 * q + 8 * lg < NV;
 
   // First product, one 16-row block of Z at a time: Z[rb] = X[rb] R[:, pair].
   constexpr int KSL = KS2 + (S::TAIL ? 1 : 0);   // slabs incl. the zero-padded tail
@@ -435,7 +442,8 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS1; ++ks) {
-      const V a = *reinterpret_cast<const V*>(xs + ((rb * KS1 + ks) * 64 + lane) * 8);
+      V a = *reinterpret_cast<const V*>(xs + ((rb * KS1 + ks) * 64 + lane) * 8);
+      if (NV < S::N && ks == KS1 - 1 && 32 * ks + 8 * lg >= NV) a = V{};   // padded k
       acc0 = Ops::mfma(a, rf[0][ks], acc0);
       acc1 = Ops::mfma(a, rf[1][ks], acc1);
     }
@@ -499,7 +507,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
       uint32_t word = 0u - Epi::kJunk;
 #pragma unroll
       for (int r = 0; r < 4; ++r) Epi::accumulate(word, yp[mb][r], rcp, r);
-      orow[(16 * mb + li) * (N / 8)] = (int32_t)word;
+      if (col_ok) orow[(16 * mb + li) * (NV / 8)] = (int32_t)word;
     }
     return;
   }
@@ -524,7 +532,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
       uint32_t word = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) word |= (uint32_t)(code[j] + 8) << (4 * j);
-      reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (N / 8) + 4 * q + lg] = (int32_t)word;
+      if (col_ok) reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (NV / 8) + 4 * q + lg] = (int32_t)word;
     } else {
       uint32_t lo4 = 0, hi4 = 0;
 #pragma unroll
@@ -533,20 +541,20 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
         hi4 |= (uint32_t)(code[4 + j] & 0xFF) << (8 * j);
       }
       v2i pair = {(int)lo4, (int)hi4};
-      *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + m * N + 32 * q + 8 * lg) = pair;
+      if (col_ok) *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + m * NV + 32 * q + 8 * lg) = pair;
     }
   }
 }
 
-template <class DT, int MB, int NP, bool PACK>
-__global__ void __launch_bounds__((FqShape<MB, NP>::WAVES * 64)) __attribute__((amdgpu_waves_per_eu(2)))
+template <class DT, int MB, int NP, bool PACK, int NV>
+__global__ void __launch_bounds__((FqShape<MB, NP, NV>::WAVES * 64)) __attribute__((amdgpu_waves_per_eu(2)))
 fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
                const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right,
                float clip, void* __restrict__ out_codes, float* __restrict__ out_scales) {
-  using S = FqShape<MB, NP>;
+  using S = FqShape<MB, NP, NV>;
   using T = typename DT::T;
   using V = typename MfmaOps<DT>::V;
-  constexpr int M = S::M, N = S::N, KS1 = S::KS1, KS2 = S::KS2;
+  constexpr int M = S::M, KS1 = S::KS1, KS2 = S::KS2;
   constexpr int NT = S::WAVES * 64;
 
   // Two X stages as distinct objects: the compiler then knows that reading one
@@ -575,7 +583,8 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
       const int rb = fr / KS1, ks = fr % KS1;
       int64_t t = g * S::TPB + ts;
       t = t < tokens ? t : tokens - 1;  // tail slots re-read a valid row; never stored
-      const T* src = x + t * x_ld + (16 * rb + li) * N + 32 * ks + 8 * lg;
+      // padded chunks (columns >= NV) re-read the row's last chunk; zeroed before use
+      const T* src = x + t * x_ld + (16 * rb + li) * NV + min(32 * ks + 8 * lg, NV - 8);
       __builtin_amdgcn_global_load_lds((const void*)src,
                                        (__attribute__((address_space(3))) void*)(stage + c * 512), 16, 0, 0);
     }
@@ -604,7 +613,10 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 #pragma unroll
     for (int ks = 0; ks < KS1; ++ks)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) rf[h][ks][j] = right[(32 * ks + 8 * lg + j) * N + n];
+      for (int j = 0; j < 8; ++j) {
+        const int k = 32 * ks + 8 * lg + j;
+        rf[h][ks][j] = (k < NV && n < NV) ? right[k * NV + n] : DT::from_f(0.0f);
+      }
   }
 
   // L, staged row-major through the free X stage with coalesced 16-byte
@@ -646,13 +658,13 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   while (g < ngroups) {
     int64_t gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf1);
-    fq_mfma_group<DT, MB, NP, PACK>(xbuf0 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
+    fq_mfma_group<DT, MB, NP, PACK, NV>(xbuf0 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
                                     out_codes, out_scales, lane, tau, q);
     g = gn;
     if (g >= ngroups) break;
     gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf0);
-    fq_mfma_group<DT, MB, NP, PACK>(xbuf1 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
+    fq_mfma_group<DT, MB, NP, PACK, NV>(xbuf1 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
                                     out_codes, out_scales, lane, tau, q);
     g = gn;
   }
@@ -1332,17 +1344,17 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
 
-template <class DT, int MB, int NP, bool PACK>
+template <class DT, int MB, int NP, bool PACK, int NV = 32 * NP>
 static int launch_mfma(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right,
                        float clip, void* out_codes, float* out_scales, hipStream_t stream) {
-  using S = FqShape<MB, NP>;
+  using S = FqShape<MB, NP, NV>;
   using T = typename DT::T;
   constexpr size_t lds = 2 * S::STAGE_ELEMS * sizeof(T);  // static LDS of the kernel
   const int per_cu = (int)std::min<size_t>(4, (160 * 1024) / (lds + 256));
   const int64_t ngroups = (tokens + S::TPB - 1) / S::TPB;
   int64_t grid = (int64_t)device_cu_count() * per_cu;
   if (grid > ngroups) grid = ngroups;
-  hipLaunchKernelGGL((fq_mfma_kernel<DT, MB, NP, PACK>), dim3((unsigned)grid), dim3(S::WAVES * 64), 0, stream,
+  hipLaunchKernelGGL((fq_mfma_kernel<DT, MB, NP, PACK, NV>), dim3((unsigned)grid), dim3(S::WAVES * 64), 0, stream,
                      reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
                      reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
   return QO_OK;
@@ -1436,6 +1448,14 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE(8, 6)   // 128 x 192  (hidden 24576)
   QO_FQ_CASE(8, 7)   // 128 x 224  (hidden 28672)
 #undef QO_FQ_CASE
+  // widths that are not a multiple of 32: computed zero-padded to 32 NP
+#define QO_FQ_CASE_NV(MB_, NP_, NV_)                                                                     \
+  if (M == 16 * (MB_) && N == (NV_))                                                                     \
+    return launch_mfma<DT, MB_, NP_, PACK, NV_>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, \
+                                                stream);
+  QO_FQ_CASE_NV(4, 3, 80)    // 64 x 80   (hidden 5120)
+  QO_FQ_CASE_NV(4, 4, 112)   // 64 x 112  (hidden 7168)
+#undef QO_FQ_CASE_NV
   *handled = false;
   return QO_OK;
 }

@@ -119,7 +119,9 @@ SHAPES = [
     (4, 128, 160, torch.float16, 1.0, False),    # N = 160 (hidden 20480)
     (2, 128, 192, torch.bfloat16, 0.9, True),    # N = 192 (hidden 24576)
     (3, 128, 224, torch.bfloat16, 0.9, True),    # N = 224 (hidden 28672)
-    (6, 64, 80, torch.float16, 0.9, True),       # generic kernel (hidden 5120)
+    (6, 64, 80, torch.float16, 0.9, True),       # N zero-padded to 96 (hidden 5120)
+    (5, 64, 80, torch.bfloat16, 1.0, False),     # the same, int8 codes
+    (7, 64, 112, torch.bfloat16, 0.9, True),     # N zero-padded to 128 (hidden 7168)
 ]
 
 
@@ -133,7 +135,7 @@ def test_quantize_shapes(gpu, t, m, n, dtype, clip, pack):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("mn", [(64, 64), (112, 128), (64, 96), (128, 224)])
+@pytest.mark.parametrize("mn", [(64, 64), (112, 128), (64, 96), (128, 224), (64, 80), (64, 112)])
 def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
     m, n = mn
     case = wl.quant_case("xcheck", 37, m, n, dtype, 0.9, True, seed=5, outlier_frac=0.005, outlier_scale=30.0)
