@@ -382,16 +382,17 @@ struct FqEpi<BF16T> {
   __device__ static inline uint32_t amax_bits(const Amax& a) { return max(a.m & 0xFFFFu, a.m >> 16); }
 };
 
-// NV: the row width in memory; N = 32 NP is the width computed, and columns
-// NV .. N - 1 are zero padding (X's padded k zeroed in registers, R's padded
-// rows and columns zero, padded codes not stored; their Y values are 0, which
-// leaves max |Y| unchanged).
-template <int MB, int NP, int NV = 32 * NP>
+// NV, MV: the token's width and height in memory; N = 32 NP and M = 16 MB are
+// computed, the rest is zero padding (X's padded columns and rows zeroed in
+// registers, R's and L's padded rows and columns zero, padded codes not
+// stored; the padded Y values are 0, which leaves max |Y| unchanged).
+template <int MB, int NP, int NV = 32 * NP, int MV = 16 * MB>
 struct FqShape {
   static constexpr int M = 16 * MB;
   static constexpr int N = 32 * NP;
-  static constexpr int F = M * NV;
+  static constexpr int F = MV * NV;
   static_assert(NV % 8 == 0 && NV > 32 * (NP - 1) && NV <= N, "valid width");
+  static_assert(MV > 16 * (MB - 1) && MV <= M, "valid height");
   static constexpr int KS1 = NP;             // 32-deep slabs of the first product (k = n')
   static constexpr int KS2 = MB / 2;         // full 32-deep slabs of the second product (k = m')
   static constexpr bool TAIL = (MB & 1) != 0; // plus one 16-deep slab when M is an odd multiple of 16
@@ -419,13 +420,13 @@ __device__ inline void wait_vmcnt() {
 
 // One token group (this wave's token slot and pair) from an X stage in LDS:
 // both products, the per-token scale and the codes.
-template <class DT, int MB, int NP, bool PACK, int NV>
+template <class DT, int MB, int NP, bool PACK, int NV, int MV>
 __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FqShape<MB, NP>::KS2 + 1],
     const typename MfmaOps<DT>::V (&rf)[2][FqShape<MB, NP>::KS1], float (*red)[NP][2], int64_t t,
     int64_t tokens, float clip, void* __restrict__ out_codes, float* __restrict__ out_scales, int lane,
     int tau, int q) {
-  using S = FqShape<MB, NP, NV>;
+  using S = FqShape<MB, NP, NV, MV>;
   using T = typename DT::T;
   using Ops = MfmaOps<DT>;
   using V = typename Ops::V;
@@ -444,6 +445,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     for (int ks = 0; ks < KS1; ++ks) {
       V a = *reinterpret_cast<const V*>(xs + ((rb * KS1 + ks) * 64 + lane) * 8);
       if (NV < S::N && ks == KS1 - 1 && 32 * ks + 8 * lg >= NV) a = V{};   // padded k
+      if (MV < S::M && rb == MB - 1 && 16 * rb + li >= MV) a = V{};        // padded row
       acc0 = Ops::mfma(a, rf[0][ks], acc0);
       acc1 = Ops::mfma(a, rf[1][ks], acc1);
     }
@@ -507,7 +509,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
       uint32_t word = 0u - Epi::kJunk;
 #pragma unroll
       for (int r = 0; r < 4; ++r) Epi::accumulate(word, yp[mb][r], rcp, r);
-      if (col_ok) orow[(16 * mb + li) * (NV / 8)] = (int32_t)word;
+      if (col_ok && 16 * mb + li < MV) orow[(16 * mb + li) * (NV / 8)] = (int32_t)word;
     }
     return;
   }
@@ -516,6 +518,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = 16 * mb + li;
+    if (m >= MV) continue;
     int code[8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -546,15 +549,15 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
   }
 }
 
-template <class DT, int MB, int NP, bool PACK, int NV>
-__global__ void __launch_bounds__((FqShape<MB, NP, NV>::WAVES * 64)) __attribute__((amdgpu_waves_per_eu(2)))
+template <class DT, int MB, int NP, bool PACK, int NV, int MV>
+__global__ void __launch_bounds__((FqShape<MB, NP, NV, MV>::WAVES * 64)) __attribute__((amdgpu_waves_per_eu(2)))
 fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
                const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right,
                float clip, void* __restrict__ out_codes, float* __restrict__ out_scales) {
-  using S = FqShape<MB, NP, NV>;
+  using S = FqShape<MB, NP, NV, MV>;
   using T = typename DT::T;
   using V = typename MfmaOps<DT>::V;
-  constexpr int M = S::M, KS1 = S::KS1, KS2 = S::KS2;
+  constexpr int KS1 = S::KS1, KS2 = S::KS2;
   constexpr int NT = S::WAVES * 64;
 
   // Two X stages as distinct objects: the compiler then knows that reading one
@@ -584,7 +587,8 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
       int64_t t = g * S::TPB + ts;
       t = t < tokens ? t : tokens - 1;  // tail slots re-read a valid row; never stored
       // padded chunks (columns >= NV) re-read the row's last chunk; zeroed before use
-      const T* src = x + t * x_ld + (16 * rb + li) * NV + min(32 * ks + 8 * lg, NV - 8);
+      // padded rows (>= MV) re-read the last row; zeroed before use
+      const T* src = x + t * x_ld + min(16 * rb + li, MV - 1) * NV + min(32 * ks + 8 * lg, NV - 8);
       __builtin_amdgcn_global_load_lds((const void*)src,
                                        (__attribute__((address_space(3))) void*)(stage + c * 512), 16, 0, 0);
     }
@@ -626,7 +630,8 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   // and, for odd M/16, the zero-padded slab lf[mb][KS2][j] = L[16(MB-1) + 4lg + j][m]
   // for j < 4.
   {
-    constexpr int CHUNKS = M * M / 8;   // 16-byte chunks of L
+    constexpr int CHUNKS = MV * MV / 8;   // whole 16-byte chunks of L (MV x MV), then the tail elements
+    constexpr int TAILE = MV * MV - 8 * CHUNKS;
     typedef int v4i_t __attribute__((ext_vector_type(4)));
     v4i_t tmp[(CHUNKS + NT - 1) / NT];
 #pragma unroll
@@ -639,32 +644,35 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
       const int c = tid + i * NT;
       if (c < CHUNKS) reinterpret_cast<v4i_t*>(xbuf1)[c] = tmp[i];
     }
+    if (TAILE > 0 && tid < TAILE) xbuf1[8 * CHUNKS + tid] = left[8 * CHUNKS + tid];
   }
   lds_barrier();
+  // L[m'][m] of the staged MV x MV rows, 0 in the padding
+  auto lval = [&](int mp, int m) { return (mp < MV && m < MV) ? xbuf1[mp * MV + m] : DT::from_f(0.0f); };
   V lf[MB][KS2 + 1];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
     for (int s = 0; s < KS2; ++s)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) lf[mb][s][j] = xbuf1[(32 * s + 16 * (j >> 2) + 4 * lg + (j & 3)) * M + 16 * mb + li];
+      for (int j = 0; j < 8; ++j) lf[mb][s][j] = lval(32 * s + 16 * (j >> 2) + 4 * lg + (j & 3), 16 * mb + li);
     // zero-padded trailing slab: m' = 16(MB-1) + 4lg + j for j < 4
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      lf[mb][KS2][j] = (S::TAIL && j < 4) ? xbuf1[(16 * (MB - 1) + 4 * lg + j) * M + 16 * mb + li] : DT::from_f(0.0f);
+      lf[mb][KS2][j] = (S::TAIL && j < 4) ? lval(16 * (MB - 1) + 4 * lg + j, 16 * mb + li) : DT::from_f(0.0f);
   }
   lds_barrier();   // xbuf1 is free again for the first prefetch
 
   while (g < ngroups) {
     int64_t gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf1);
-    fq_mfma_group<DT, MB, NP, PACK, NV>(xbuf0 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
+    fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf0 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
                                     out_codes, out_scales, lane, tau, q);
     g = gn;
     if (g >= ngroups) break;
     gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf0);
-    fq_mfma_group<DT, MB, NP, PACK, NV>(xbuf1 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
+    fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf1 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
                                     out_codes, out_scales, lane, tau, q);
     g = gn;
   }
@@ -1344,17 +1352,17 @@ fq_duo_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
 
-template <class DT, int MB, int NP, bool PACK, int NV = 32 * NP>
+template <class DT, int MB, int NP, bool PACK, int NV = 32 * NP, int MV = 16 * MB>
 static int launch_mfma(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right,
                        float clip, void* out_codes, float* out_scales, hipStream_t stream) {
-  using S = FqShape<MB, NP, NV>;
+  using S = FqShape<MB, NP, NV, MV>;
   using T = typename DT::T;
   constexpr size_t lds = 2 * S::STAGE_ELEMS * sizeof(T);  // static LDS of the kernel
   const int per_cu = (int)std::min<size_t>(4, (160 * 1024) / (lds + 256));
   const int64_t ngroups = (tokens + S::TPB - 1) / S::TPB;
   int64_t grid = (int64_t)device_cu_count() * per_cu;
   if (grid > ngroups) grid = ngroups;
-  hipLaunchKernelGGL((fq_mfma_kernel<DT, MB, NP, PACK, NV>), dim3((unsigned)grid), dim3(S::WAVES * 64), 0, stream,
+  hipLaunchKernelGGL((fq_mfma_kernel<DT, MB, NP, PACK, NV, MV>), dim3((unsigned)grid), dim3(S::WAVES * 64), 0, stream,
                      reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
                      reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
   return QO_OK;
@@ -1455,7 +1463,17 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
                                                 stream);
   QO_FQ_CASE_NV(4, 3, 80)    // 64 x 80   (hidden 5120)
   QO_FQ_CASE_NV(4, 4, 112)   // 64 x 112  (hidden 7168)
+  QO_FQ_CASE_NV(8, 5, 144)   // 128 x 144 (hidden 18432)
 #undef QO_FQ_CASE_NV
+  // heights that are not a multiple of 16: computed zero-padded to 16 MB
+#define QO_FQ_CASE_MV(MB_, NP_, MV_)                                                                          \
+  if (M == (MV_) && N == 32 * (NP_))                                                                          \
+    return launch_mfma<DT, MB_, NP_, PACK, 32 * (NP_), MV_>(x, tokens, x_ld, left, right, clip, out_codes,    \
+                                                            out_scales, stream);
+  QO_FQ_CASE_MV(4, 2, 56)    // 56 x 64   (hidden 3584)
+  QO_FQ_CASE_MV(6, 4, 86)    // 86 x 128  (hidden 11008)
+  QO_FQ_CASE_MV(7, 4, 108)   // 108 x 128 (hidden 13824)
+#undef QO_FQ_CASE_MV
   *handled = false;
   return QO_OK;
 }

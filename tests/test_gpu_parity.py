@@ -122,6 +122,11 @@ SHAPES = [
     (6, 64, 80, torch.float16, 0.9, True),       # N zero-padded to 96 (hidden 5120)
     (5, 64, 80, torch.bfloat16, 1.0, False),     # the same, int8 codes
     (7, 64, 112, torch.bfloat16, 0.9, True),     # N zero-padded to 128 (hidden 7168)
+    (9, 56, 64, torch.float16, 0.9, True),       # M zero-padded to 64 (hidden 3584)
+    (5, 86, 128, torch.bfloat16, 0.9, True),     # M zero-padded to 96, L staged with a partial chunk (11008)
+    (4, 86, 128, torch.float16, 1.0, False),     # the same, int8 codes
+    (6, 108, 128, torch.bfloat16, 1.0, True),    # M zero-padded to 112 (hidden 13824)
+    (3, 128, 144, torch.bfloat16, 0.9, True),    # N zero-padded to 160 (hidden 18432)
 ]
 
 
@@ -135,7 +140,8 @@ def test_quantize_shapes(gpu, t, m, n, dtype, clip, pack):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("mn", [(64, 64), (112, 128), (64, 96), (128, 224), (64, 80), (64, 112)])
+@pytest.mark.parametrize("mn", [(64, 64), (112, 128), (64, 96), (128, 224), (64, 80), (64, 112), (56, 64), (86, 128),
+                                (108, 128)])
 def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
     m, n = mn
     case = wl.quant_case("xcheck", 37, m, n, dtype, 0.9, True, seed=5, outlier_frac=0.005, outlier_scale=30.0)
