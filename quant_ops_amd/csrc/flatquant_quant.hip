@@ -393,6 +393,9 @@ struct FqShape {
   static constexpr int F = MV * NV;
   static_assert(NV % 8 == 0 && NV > 32 * (NP - 1) && NV <= N, "valid width");
   static_assert(MV > 16 * (MB - 1) && MV <= M, "valid height");
+  // L's fragments (MB (KS2 + 1) of them, 4 VGPRs each) stay in LDS instead of
+  // VGPRs where they would not fit beside R's (2 KS1) and the accumulators.
+  static constexpr bool LF_LDS = MB * (MB / 2 + 1) + 2 * NP > 32 || MV != M;
   static constexpr int KS1 = NP;             // 32-deep slabs of the first product (k = n')
   static constexpr int KS2 = MB / 2;         // full 32-deep slabs of the second product (k = m')
   static constexpr bool TAIL = (MB & 1) != 0; // plus one 16-deep slab when M is an odd multiple of 16
@@ -423,6 +426,7 @@ __device__ inline void wait_vmcnt() {
 template <class DT, int MB, int NP, bool PACK, int NV, int MV>
 __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FqShape<MB, NP>::KS2 + 1],
+    const unsigned char* lf_lds,
     const typename MfmaOps<DT>::V (&rf)[2][FqShape<MB, NP>::KS1], float (*red)[NP][2], int64_t t,
     int64_t tokens, float clip, void* __restrict__ out_codes, float* __restrict__ out_scales, int lane,
     int tau, int q) {
@@ -473,8 +477,11 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KSL; ++s) {
-      acc0 = Ops::mfma(zp[0][s], lf[mb][s], acc0);
-      acc1 = Ops::mfma(zp[1][s], lf[mb][s], acc1);
+      V lfv;
+      if constexpr (S::LF_LDS) lfv = *reinterpret_cast<const V*>(lf_lds + (mb * (KS2 + 1) + s) * 1024 + 16 * lane);
+      else lfv = lf[mb][s];
+      acc0 = Ops::mfma(zp[0][s], lfv, acc0);
+      acc1 = Ops::mfma(zp[1][s], lfv, acc1);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -564,6 +571,7 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   // stage does not depend on the LDS-DMA still writing the other.
   __shared__ __align__(16) T xbuf0[S::STAGE_ELEMS];
   __shared__ __align__(16) T xbuf1[S::STAGE_ELEMS];
+  __shared__ __align__(16) unsigned char lf_lds[S::LF_LDS ? MB * (KS2 + 1) * 1024 : 16];
   __shared__ float red[S::TPB][NP][2];
 
   const int tid = threadIdx.x;
@@ -650,29 +658,37 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   // L[m'][m] of the staged MV x MV rows, 0 in the padding
   auto lval = [&](int mp, int m) { return (mp < MV && m < MV) ? xbuf1[mp * MV + m] : DT::from_f(0.0f); };
   V lf[MB][KS2 + 1];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-    for (int s = 0; s < KS2; ++s)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) lf[mb][s][j] = lval(32 * s + 16 * (j >> 2) + 4 * lg + (j & 3), 16 * mb + li);
-    // zero-padded trailing slab: m' = 16(MB-1) + 4lg + j for j < 4
+  auto lfrag = [&](int mb, int s) {   // fragment (mb, s); s = KS2 is the zero-padded trailing slab
+    V v;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      lf[mb][KS2][j] = (S::TAIL && j < 4) ? lval(16 * (MB - 1) + 4 * lg + j, 16 * mb + li) : DT::from_f(0.0f);
+      v[j] = s < KS2 ? lval(32 * s + 16 * (j >> 2) + 4 * lg + (j & 3), 16 * mb + li)
+                     : (S::TAIL && j < 4) ? lval(16 * (MB - 1) + 4 * lg + j, 16 * mb + li) : DT::from_f(0.0f);
+    return v;
+  };
+  if constexpr (S::LF_LDS) {
+    // the waves split the fragments; the barrier below makes them visible
+#pragma unroll 1
+    for (int fr = wave; fr < MB * (KS2 + 1); fr += S::WAVES)
+      *reinterpret_cast<V*>(lf_lds + fr * 1024 + 16 * lane) = lfrag(fr / (KS2 + 1), fr % (KS2 + 1));
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int s = 0; s <= KS2; ++s) lf[mb][s] = lfrag(mb, s);
   }
   lds_barrier();   // xbuf1 is free again for the first prefetch
 
   while (g < ngroups) {
     int64_t gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf1);
-    fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf0 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
+    fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf0 + tau * S::XFRAGS * 512, lf, lf_lds, rf, red, g * S::TPB + tau, tokens, clip,
                                     out_codes, out_scales, lane, tau, q);
     g = gn;
     if (g >= ngroups) break;
     gn = g + gridDim.x;
     prefetch_and_wait(gn, xbuf0);
-    fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf1 + tau * S::XFRAGS * 512, lf, rf, red, g * S::TPB + tau, tokens, clip,
+    fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf1 + tau * S::XFRAGS * 512, lf, lf_lds, rf, red, g * S::TPB + tau, tokens, clip,
                                     out_codes, out_scales, lane, tau, q);
     g = gn;
   }
