@@ -1425,13 +1425,27 @@ static bool fq_allow_wave() {
   return !(e && e[0] == '1');
 }
 
+// QO_FQ_NO_FEW=1 keeps the one-wave and pair kernels at any token count
+// (tests use it to cross-check them against the workgroup kernel on small
+// inputs).
+static bool fq_route_few() {
+  const char* e = getenv("QO_FQ_NO_FEW");
+  return !(e && e[0] == '1');
+}
+
 template <class DT, bool PACK>
 static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_ld, const void* left,
                          const void* right, float clip, void* out_codes, float* out_scales,
                          hipStream_t stream, bool* handled) {
   *handled = true;
+  // Up to a few hundred tokens the workgroup kernel (fq_mfma_kernel, one
+  // token per group of 2-4 waves) finishes sooner than the one-wave and pair
+  // kernels, whose per-token chain is longer; measured crossovers: 64 x 64
+  // after 512 tokens (16 tokens bf16: 5.2 vs 6.4 us), 32 x 64 and 64 x 128
+  // after 256. Wider pair-kernel shapes keep the pair kernel at any count.
+  const bool few = fq_route_few() && tokens <= (M == 64 && N == 64 ? 512 : 256);
   // the wave kernel takes the scale from max |Y|, which needs clip > 0
-  if (fq_allow_wave() && clip > 0.f && clip <= 3.4e38f) {
+  if (fq_allow_wave() && clip > 0.f && clip <= 3.4e38f && !few) {
 #define QO_FQ_WAVE_CASE(MB_, NQ_)                                                                    \
     if (M == 16 * (MB_) && N == 32 * (NQ_))                                                          \
       return launch_wave<DT, MB_, NQ_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, \
@@ -1443,7 +1457,7 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
 #undef QO_FQ_WAVE_CASE
   }
   // the pair kernel takes its scale from max |Y| as well
-  if (fq_allow_duo() && clip > 0.f && clip <= 3.4e38f && N == 128) {
+  if (fq_allow_duo() && clip > 0.f && clip <= 3.4e38f && N == 128 && !(few && M == 64)) {
 #define QO_FQ_DUO_CASE(MB_)                                                                                  \
     if (M == 16 * (MB_))                                                                                     \
       return launch_duo<DT, MB_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream);

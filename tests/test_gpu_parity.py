@@ -167,6 +167,7 @@ def test_quantize_wave_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack,
                          outlier_scale=20.0)
     case.x[tokens // 2].zero_()
     _say(f"wave vs group kernel T={tokens} {m}x{n} {dtype} pack={pack}")
+    monkeypatch.setenv("QO_FQ_NO_FEW", "1")        # the wave kernel also below its token threshold
     q1, s1 = run_capi_quant(case, gpu)
     monkeypatch.setenv("QO_FQ_NO_WAVE", "1")
     q2, s2 = run_capi_quant(case, gpu)
@@ -187,6 +188,7 @@ def test_quantize_pair_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack,
                          outlier_scale=30.0)
     case.x[tokens // 2].zero_()
     _say(f"pair vs group kernel T={tokens} {m}x{n} {dtype} pack={pack}")
+    monkeypatch.setenv("QO_FQ_NO_FEW", "1")        # the pair kernel also below its token threshold
     q1, s1 = run_capi_quant(case, gpu)
     monkeypatch.setenv("QO_FQ_NO_DUO", "1")
     q2, s2 = run_capi_quant(case, gpu)
