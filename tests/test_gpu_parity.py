@@ -127,6 +127,9 @@ SHAPES = [
     (4, 86, 128, torch.float16, 1.0, False),     # the same, int8 codes
     (6, 108, 128, torch.bfloat16, 1.0, True),    # M zero-padded to 112 (hidden 13824)
     (3, 128, 144, torch.bfloat16, 0.9, True),    # N zero-padded to 160 (hidden 18432)
+    (3000, 64, 80, torch.bfloat16, 0.9, True),   # padded width, groups loop over many tokens
+    (1500, 86, 128, torch.float16, 1.0, True),   # padded height, the same
+    (700, 128, 224, torch.bfloat16, 0.9, True),  # L fragments in LDS, the same
 ]
 
 
