@@ -43,9 +43,13 @@ HIP_FLAGS = [
 ]
 # Per-file additions. The quantize kernels keep MFMA results in VGPRs (the AGPR
 # form costs a v_accvgpr_read per result element their epilogues consume); the
-# GEMM lets the compiler place its accumulators, which measured faster.
+# GEMM lets the compiler place its accumulators, which measured faster. The
+# quantize kernels also take their first 16 argument dwords preloaded into
+# SGPRs (no scalar load before the first DMA issue: 1-2% on launches of a few
+# microseconds); the GEMM measured no gain from it.
 FILE_FLAGS = {
-    "flatquant_quant.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "flatquant_quant.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1",
+                            "-mllvm", "-amdgpu-kernarg-preload-count=16"],
 }
 
 
