@@ -1478,7 +1478,7 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE(8, 4)   // 128 x 128  (hidden 16384)
   QO_FQ_CASE(2, 1)   // 32 x 32    (hidden 1024)
   QO_FQ_CASE(3, 2)   // 48 x 64    (hidden 3072)
-  QO_FQ_CASE(5, 2)   // 80 x 64    (get_decompose_dim(5120) is 64 x 80, which takes the generic kernel)
+  QO_FQ_CASE(5, 2)   // 80 x 64
   QO_FQ_CASE(6, 4)   // 96 x 128   (hidden 12288)
   QO_FQ_CASE(4, 3)   // 64 x 96    (hidden 6144)
   QO_FQ_CASE(5, 4)   // 80 x 128   (hidden 10240)
@@ -1494,6 +1494,9 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE_NV(4, 3, 80)    // 64 x 80   (hidden 5120)
   QO_FQ_CASE_NV(4, 4, 112)   // 64 x 112  (hidden 7168)
   QO_FQ_CASE_NV(8, 5, 144)   // 128 x 144 (hidden 18432)
+  QO_FQ_CASE_NV(2, 2, 48)    // 32 x 48   (hidden 1536)
+  QO_FQ_CASE_NV(4, 3, 88)    // 64 x 88   (hidden 5632)
+  QO_FQ_CASE_NV(5, 4, 112)   // 80 x 112  (hidden 8960)
 #undef QO_FQ_CASE_NV
   // heights that are not a multiple of 16: computed zero-padded to 16 MB
 #define QO_FQ_CASE_MV(MB_, NP_, MV_)                                                                          \
@@ -1503,6 +1506,9 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE_MV(4, 2, 56)    // 56 x 64   (hidden 3584)
   QO_FQ_CASE_MV(6, 4, 86)    // 86 x 128  (hidden 11008)
   QO_FQ_CASE_MV(7, 4, 108)   // 108 x 128 (hidden 13824)
+  QO_FQ_CASE_MV(3, 2, 40)    // 40 x 64   (hidden 2560)
+  QO_FQ_CASE_MV(5, 3, 72)    // 72 x 96   (hidden 6912)
+  QO_FQ_CASE_MV(5, 4, 76)    // 76 x 128  (hidden 9728)
 #undef QO_FQ_CASE_MV
   *handled = false;
   return QO_OK;

@@ -127,6 +127,12 @@ SHAPES = [
     (4, 86, 128, torch.float16, 1.0, False),     # the same, int8 codes
     (6, 108, 128, torch.bfloat16, 1.0, True),    # M zero-padded to 112 (hidden 13824)
     (3, 128, 144, torch.bfloat16, 0.9, True),    # N zero-padded to 160 (hidden 18432)
+    (5, 32, 48, torch.float16, 0.9, True),       # N zero-padded to 64 (hidden 1536)
+    (4, 64, 88, torch.bfloat16, 1.0, False),     # N zero-padded to 96 (hidden 5632), int8 codes
+    (6, 80, 112, torch.bfloat16, 0.9, True),     # odd M / 16, N zero-padded to 128 (hidden 8960)
+    (7, 40, 64, torch.float16, 0.9, True),       # M zero-padded to 48 (hidden 2560)
+    (5, 72, 96, torch.bfloat16, 0.9, True),      # M zero-padded to 80, three-wave groups (hidden 6912)
+    (3, 76, 128, torch.float16, 1.0, False),     # M zero-padded to 80 (hidden 9728), int8 codes
     (3000, 64, 80, torch.bfloat16, 0.9, True),   # padded width, groups loop over many tokens
     (1500, 86, 128, torch.float16, 1.0, True),   # padded height, the same
     (700, 128, 224, torch.bfloat16, 0.9, True),  # L fragments in LDS, the same
@@ -144,7 +150,7 @@ def test_quantize_shapes(gpu, t, m, n, dtype, clip, pack):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mn", [(64, 64), (112, 128), (64, 96), (128, 224), (64, 80), (64, 112), (56, 64), (86, 128),
-                                (108, 128)])
+                                (108, 128), (32, 48), (64, 88), (80, 112), (40, 64), (72, 96), (76, 128)])
 def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
     m, n = mn
     case = wl.quant_case("xcheck", 37, m, n, dtype, 0.9, True, seed=5, outlier_frac=0.005, outlier_scale=30.0)
