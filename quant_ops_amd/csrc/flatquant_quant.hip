@@ -386,12 +386,16 @@ struct FqEpi<BF16T> {
 // computed, the rest is zero padding (X's padded columns and rows zeroed in
 // registers, R's and L's padded rows and columns zero, padded codes not
 // stored; the padded Y values are 0, which leaves max |Y| unchanged).
+// NV % 8 == 4 (SPLIT): odd rows start 8 bytes past a 16-byte boundary, so X
+// is copied in 4-byte pieces and codes are stored in 16-bit (packed) or
+// 4-byte (int8) pieces; the row's last 8-column chunk is half padding.
 template <int MB, int NP, int NV = 32 * NP, int MV = 16 * MB>
 struct FqShape {
   static constexpr int M = 16 * MB;
   static constexpr int N = 32 * NP;
   static constexpr int F = MV * NV;
-  static_assert(NV % 8 == 0 && NV > 32 * (NP - 1) && NV <= N, "valid width");
+  static_assert(NV % 4 == 0 && NV > 32 * (NP - 1) && NV <= N, "valid width");
+  static constexpr bool SPLIT = NV % 8 != 0;
   static_assert(MV > 16 * (MB - 1) && MV <= M, "valid height");
   // L's fragments (MB (KS2 + 1) of them, 4 VGPRs each) stay in LDS instead of
   // VGPRs where they would not fit beside R's (2 KS1) and the accumulators.
@@ -406,7 +410,8 @@ struct FqShape {
   static constexpr int TPB = NP >= 4 ? 1 : 4 / NP;   // tokens per group
   static constexpr int WAVES = NP * TPB;
   static constexpr int STAGE_FRAGS = TPB * XFRAGS;
-  static constexpr int DMA_PER_WAVE = STAGE_FRAGS / WAVES;   // == MB
+  static constexpr int FRAGS_PER_WAVE = STAGE_FRAGS / WAVES;   // == MB
+  static constexpr int DMA_PER_WAVE = (SPLIT ? 4 : 1) * FRAGS_PER_WAVE;
   static constexpr int STAGE_ELEMS = STAGE_FRAGS * 512;
   static_assert(STAGE_FRAGS % WAVES == 0, "X fragments must split evenly over waves");
   static_assert(M * M <= STAGE_ELEMS, "L must fit in one X stage while it is staged");
@@ -437,7 +442,9 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
   constexpr int F = S::F, KS1 = S::KS1, KS2 = S::KS2;
   const int li = lane & 15, lg = lane >> 4;
   // this lane's 8 columns of its pair: stored only inside the valid width
+  // (with SPLIT the last chunk's first 4 columns only: col_hi false)
   const bool col_ok = 32 * q + 8 * lg < NV;
+  const bool col_hi = 32 * q + 8 * lg + 8 <= NV;
 
   // First product, one 16-row block of Z at a time: Z[rb] = X[rb] R[:, pair].
   constexpr int KSL = KS2 + (S::TAIL ? 1 : 0);   // slabs incl. the zero-padded tail
@@ -449,6 +456,10 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     for (int ks = 0; ks < KS1; ++ks) {
       V a = *reinterpret_cast<const V*>(xs + ((rb * KS1 + ks) * 64 + lane) * 8);
       if (NV < S::N && ks == KS1 - 1 && 32 * ks + 8 * lg >= NV) a = V{};   // padded k
+      if (S::SPLIT && ks == KS1 - 1 && 32 * ks + 8 * lg + 4 == NV) {         // half-padded chunk
+#pragma unroll
+        for (int j = 4; j < 8; ++j) a[j] = DT::from_f(0.0f);
+      }
       if (MV < S::M && rb == MB - 1 && 16 * rb + li >= MV) a = V{};        // padded row
       acc0 = Ops::mfma(a, rf[0][ks], acc0);
       acc1 = Ops::mfma(a, rf[1][ks], acc1);
@@ -516,7 +527,18 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
       uint32_t word = 0u - Epi::kJunk;
 #pragma unroll
       for (int r = 0; r < 4; ++r) Epi::accumulate(word, yp[mb][r], rcp, r);
-      if (col_ok && 16 * mb + li < MV) orow[(16 * mb + li) * (NV / 8)] = (int32_t)word;
+      if constexpr (S::SPLIT) {
+        // nibble offset t F + m NV + 8 (4q + lg) is a multiple of 4: two 16-bit
+        // halves; 16 rows further on is 4 NV halves further on
+        uint16_t* o16 = reinterpret_cast<uint16_t*>(out_codes) + t * (F / 4) + (li * NV + 32 * q + 8 * lg) / 4 +
+                        mb * (4 * NV);
+        if (col_ok && 16 * mb + li < MV) {
+          o16[0] = (uint16_t)word;
+          if (col_hi) o16[1] = (uint16_t)(word >> 16);
+        }
+      } else {
+        if (col_ok && 16 * mb + li < MV) orow[(16 * mb + li) * (NV / 8)] = (int32_t)word;
+      }
     }
     return;
   }
@@ -542,7 +564,15 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
       uint32_t word = 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) word |= (uint32_t)(code[j] + 8) << (4 * j);
-      if (col_ok) reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (NV / 8) + 4 * q + lg] = (int32_t)word;
+      if constexpr (S::SPLIT) {
+        uint16_t* o16 = reinterpret_cast<uint16_t*>(out_codes) + t * (F / 4) + (m * NV + 32 * q + 8 * lg) / 4;
+        if (col_ok) {
+          o16[0] = (uint16_t)word;
+          if (col_hi) o16[1] = (uint16_t)(word >> 16);
+        }
+      } else {
+        if (col_ok) reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (NV / 8) + 4 * q + lg] = (int32_t)word;
+      }
     } else {
       uint32_t lo4 = 0, hi4 = 0;
 #pragma unroll
@@ -550,8 +580,16 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
         lo4 |= (uint32_t)(code[j] & 0xFF) << (8 * j);
         hi4 |= (uint32_t)(code[4 + j] & 0xFF) << (8 * j);
       }
-      v2i pair = {(int)lo4, (int)hi4};
-      if (col_ok) *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + m * NV + 32 * q + 8 * lg) = pair;
+      int8_t* ob = reinterpret_cast<int8_t*>(out_codes) + t * F + m * NV + 32 * q + 8 * lg;
+      if constexpr (S::SPLIT) {   // 4-byte aligned
+        if (col_ok) {
+          *reinterpret_cast<int32_t*>(ob) = (int32_t)lo4;
+          if (col_hi) *reinterpret_cast<int32_t*>(ob + 4) = (int32_t)hi4;
+        }
+      } else {
+        v2i pair = {(int)lo4, (int)hi4};
+        if (col_ok) *reinterpret_cast<v2i*>(ob) = pair;
+      }
     }
   }
 }
@@ -584,21 +622,41 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 
   // LDS-DMA of one token group into a stage. Fragment c of the stage is token
   // slot c / XFRAGS, block (rb, ks); lane l fetches X[16rb + l%16][32ks + 8(l/16) .. +7]
-  // (16 bytes), which the hardware writes to fragment base + 16*l.
+  // (16 bytes), which the hardware writes to fragment base + 16*l. With SPLIT
+  // each fragment takes four 4-byte copies: copy h, lane l fetches dword l%4 of
+  // fragment lane 16h + l/4, i.e. X[16rb + l/4][32ks + 8h + 2(l%4) .. +1], which
+  // lands at fragment base + 256h + 4l = base + 16(16h + l/4) + 4(l%4).
   const int64_t ngroups = (tokens + S::TPB - 1) / S::TPB;
   auto issue = [&](int64_t g, T* stage) {
 #pragma unroll
-    for (int i = 0; i < S::DMA_PER_WAVE; ++i) {
+    for (int i = 0; i < S::FRAGS_PER_WAVE; ++i) {
       const int c = wave + i * S::WAVES;
       const int ts = c / S::XFRAGS, fr = c % S::XFRAGS;
       const int rb = fr / KS1, ks = fr % KS1;
       int64_t t = g * S::TPB + ts;
       t = t < tokens ? t : tokens - 1;  // tail slots re-read a valid row; never stored
-      // padded chunks (columns >= NV) re-read the row's last chunk; zeroed before use
+      // padded chunks (columns >= NV) re-read the row's last chunk (last dword
+      // with SPLIT); zeroed before use
       // padded rows (>= MV) re-read the last row; zeroed before use
-      const T* src = x + t * x_ld + min(16 * rb + li, MV - 1) * NV + min(32 * ks + 8 * lg, NV - 8);
-      __builtin_amdgcn_global_load_lds((const void*)src,
-                                       (__attribute__((address_space(3))) void*)(stage + c * 512), 16, 0, 0);
+      if constexpr (S::SPLIT) {
+        // offsets recomputed at every issue from an opaque lane copy: 4 MB
+        // addresses held across the token loop would not fit in VGPRs
+        int l = lane;
+        asm volatile("" : "+v"(l));
+        const int off = min(16 * rb + (l >> 2), MV - 1) * NV + 2 * (l & 3);
+        const T* xt = x + t * x_ld;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const T* src = xt + min(off + 32 * ks + 8 * h, min(16 * rb + (l >> 2), MV - 1) * NV + NV - 2);
+          __builtin_amdgcn_global_load_lds((const void*)src,
+                                           (__attribute__((address_space(3))) void*)(stage + c * 512 + h * 128), 4,
+                                           0, 0);
+        }
+      } else {
+        const T* src = x + t * x_ld + min(16 * rb + li, MV - 1) * NV + min(32 * ks + 8 * lg, NV - 8);
+        __builtin_amdgcn_global_load_lds((const void*)src,
+                                         (__attribute__((address_space(3))) void*)(stage + c * 512), 16, 0, 0);
+      }
     }
   };
   // Before reading a stage: issue the next group into the other stage (past
@@ -1497,6 +1555,8 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE_NV(2, 2, 48)    // 32 x 48   (hidden 1536)
   QO_FQ_CASE_NV(4, 3, 88)    // 64 x 88   (hidden 5632)
   QO_FQ_CASE_NV(5, 4, 112)   // 80 x 112  (hidden 8960)
+  QO_FQ_CASE_NV(8, 5, 148)   // 128 x 148 (hidden 18944; 16-bit code halves)
+  QO_FQ_CASE_NV(8, 6, 172)   // 128 x 172 (hidden 22016; 16-bit code halves)
 #undef QO_FQ_CASE_NV
   // heights that are not a multiple of 16: computed zero-padded to 16 MB
 #define QO_FQ_CASE_MV(MB_, NP_, MV_)                                                                          \

@@ -133,6 +133,10 @@ SHAPES = [
     (7, 40, 64, torch.float16, 0.9, True),       # M zero-padded to 48 (hidden 2560)
     (5, 72, 96, torch.bfloat16, 0.9, True),      # M zero-padded to 80, three-wave groups (hidden 6912)
     (3, 76, 128, torch.float16, 1.0, False),     # M zero-padded to 80 (hidden 9728), int8 codes
+    (5, 128, 148, torch.bfloat16, 0.9, True),    # N = 148 (hidden 18944): rows 8-byte aligned, 16-bit code halves
+    (4, 128, 148, torch.float16, 1.0, False),    # the same, int8 codes in 4-byte pieces
+    (3, 128, 172, torch.float16, 0.9, True),     # N = 172 (hidden 22016)
+    (1100, 128, 148, torch.float16, 0.9, True),  # 8-byte aligned rows over many tokens
     (3000, 64, 80, torch.bfloat16, 0.9, True),   # padded width, groups loop over many tokens
     (1500, 86, 128, torch.float16, 1.0, True),   # padded height, the same
     (700, 128, 224, torch.bfloat16, 0.9, True),  # L fragments in LDS, the same
@@ -150,7 +154,8 @@ def test_quantize_shapes(gpu, t, m, n, dtype, clip, pack):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mn", [(64, 64), (112, 128), (64, 96), (128, 224), (64, 80), (64, 112), (56, 64), (86, 128),
-                                (108, 128), (32, 48), (64, 88), (80, 112), (40, 64), (72, 96), (76, 128)])
+                                (108, 128), (32, 48), (64, 88), (80, 112), (40, 64), (72, 96), (76, 128),
+                                (128, 148), (128, 172)])
 def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
     m, n = mn
     case = wl.quant_case("xcheck", 37, m, n, dtype, 0.9, True, seed=5, outlier_frac=0.005, outlier_scale=30.0)
