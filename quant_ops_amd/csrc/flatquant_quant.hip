@@ -403,6 +403,10 @@ struct FqShape {
   static constexpr int KS1 = NP;             // 32-deep slabs of the first product (k = n')
   static constexpr int KS2 = MB / 2;         // full 32-deep slabs of the second product (k = m')
   static constexpr bool TAIL = (MB & 1) != 0; // plus one 16-deep slab when M is an odd multiple of 16
+  static constexpr int KSL = KS2 + (TAIL ? 1 : 0);   // slabs read, incl. the zero-padded tail
+  // L's fragments in LDS at stride KS2 + 1 per row block; for even MB the
+  // last one (a zero slab never read) is left out of the allocation
+  static constexpr int LF_FRAGS = MB * (KS2 + 1) - (TAIL ? 0 : 1);
   static constexpr int XFRAGS = MB * KS1;    // 1 KiB A fragments per token
   // Four waves per workgroup: one token per group at N = 128, two at N = 64,
   // four at N = 32. Small workgroups (X double buffer only, L in VGPRs) let
@@ -447,7 +451,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
   const bool col_hi = 32 * q + 8 * lg + 8 <= NV;
 
   // First product, one 16-row block of Z at a time: Z[rb] = X[rb] R[:, pair].
-  constexpr int KSL = KS2 + (S::TAIL ? 1 : 0);   // slabs incl. the zero-padded tail
+  constexpr int KSL = S::KSL;
   V zp[2][KS2 + 1];   // 32-deep slabs of Z^T
 #pragma unroll
   for (int rb = 0; rb < MB; ++rb) {
@@ -609,7 +613,7 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   // stage does not depend on the LDS-DMA still writing the other.
   __shared__ __align__(16) T xbuf0[S::STAGE_ELEMS];
   __shared__ __align__(16) T xbuf1[S::STAGE_ELEMS];
-  __shared__ __align__(16) unsigned char lf_lds[S::LF_LDS ? MB * (KS2 + 1) * 1024 : 16];
+  __shared__ __align__(16) unsigned char lf_lds[S::LF_LDS ? S::LF_FRAGS * 1024 : 16];
   __shared__ float red[S::TPB][NP][2];
 
   const int tid = threadIdx.x;
@@ -727,7 +731,7 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   if constexpr (S::LF_LDS) {
     // the waves split the fragments; the barrier below makes them visible
 #pragma unroll 1
-    for (int fr = wave; fr < MB * (KS2 + 1); fr += S::WAVES)
+    for (int fr = wave; fr < S::LF_FRAGS; fr += S::WAVES)
       *reinterpret_cast<V*>(lf_lds + fr * 1024 + 16 * lane) = lfrag(fr / (KS2 + 1), fr % (KS2 + 1));
   } else {
 #pragma unroll
@@ -1543,6 +1547,8 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE(8, 5)   // 128 x 160  (hidden 20480)
   QO_FQ_CASE(8, 6)   // 128 x 192  (hidden 24576)
   QO_FQ_CASE(8, 7)   // 128 x 224  (hidden 28672)
+  QO_FQ_CASE(9, 6)   // 144 x 192  (hidden 27648)
+  QO_FQ_CASE(10, 5)  // 160 x 160  (hidden 25600)
 #undef QO_FQ_CASE
   // widths that are not a multiple of 32: computed zero-padded to 32 NP
 #define QO_FQ_CASE_NV(MB_, NP_, NV_)                                                                     \
