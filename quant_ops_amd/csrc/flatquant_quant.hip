@@ -386,15 +386,16 @@ struct FqEpi<BF16T> {
 // computed, the rest is zero padding (X's padded columns and rows zeroed in
 // registers, R's and L's padded rows and columns zero, padded codes not
 // stored; the padded Y values are 0, which leaves max |Y| unchanged).
-// NV % 8 == 4 (SPLIT): odd rows start 8 bytes past a 16-byte boundary, so X
-// is copied in 4-byte pieces and codes are stored in 16-bit (packed) or
-// 4-byte (int8) pieces; the row's last 8-column chunk is half padding.
+// NV % 8 != 0 (SPLIT; NV even): rows start off 16-byte boundaries, so X is
+// copied in 4-byte pieces, the row's last 8-column chunk is partly padding,
+// and codes are stored in pieces as aligned as the row offset allows: 16-bit
+// (packed) or 4-byte (int8) for NV % 4 == 0, bytes or 16-bit otherwise.
 template <int MB, int NP, int NV = 32 * NP, int MV = 16 * MB>
 struct FqShape {
   static constexpr int M = 16 * MB;
   static constexpr int N = 32 * NP;
   static constexpr int F = MV * NV;
-  static_assert(NV % 4 == 0 && NV > 32 * (NP - 1) && NV <= N, "valid width");
+  static_assert(NV % 2 == 0 && NV > 32 * (NP - 1) && NV <= N, "valid width");
   static constexpr bool SPLIT = NV % 8 != 0;
   static_assert(MV > 16 * (MB - 1) && MV <= M, "valid height");
   // L's fragments (MB (KS2 + 1) of them, 4 VGPRs each) stay in LDS instead of
@@ -430,6 +431,36 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Codes of one lane's 8 columns (rem of them inside the row, rem > 0) where
+// the row offset in a SPLIT shape allows only partial alignment. Packed: 8
+// nibbles in `word`, at a byte address that is 2-byte aligned when
+// NV % 4 == 0. int8: 8 bytes in lo4 / hi4, at an address 4-byte aligned when
+// NV % 4 == 0, 2-byte aligned otherwise.
+template <int NV>
+__device__ inline void fq_store_packed_split(uint8_t* o, uint32_t word, int rem) {
+  if constexpr (NV % 4 == 0) {
+    reinterpret_cast<uint16_t*>(o)[0] = (uint16_t)word;
+    if (rem >= 8) reinterpret_cast<uint16_t*>(o)[1] = (uint16_t)(word >> 16);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (2 * k + 2 <= rem) o[k] = (uint8_t)(word >> (8 * k));
+  }
+}
+
+template <int NV>
+__device__ inline void fq_store_int8_split(int8_t* o, uint32_t lo4, uint32_t hi4, int rem) {
+  if constexpr (NV % 4 == 0) {
+    *reinterpret_cast<int32_t*>(o) = (int32_t)lo4;
+    if (rem >= 8) *reinterpret_cast<int32_t*>(o + 4) = (int32_t)hi4;
+  } else {
+    const uint32_t h[4] = {lo4 & 0xFFFFu, lo4 >> 16, hi4 & 0xFFFFu, hi4 >> 16};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (2 * k + 2 <= rem) reinterpret_cast<uint16_t*>(o)[k] = (uint16_t)h[k];
+  }
+}
+
 // One token group (this wave's token slot and pair) from an X stage in LDS:
 // both products, the per-token scale and the codes.
 template <class DT, int MB, int NP, bool PACK, int NV, int MV>
@@ -446,9 +477,9 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
   constexpr int F = S::F, KS1 = S::KS1, KS2 = S::KS2;
   const int li = lane & 15, lg = lane >> 4;
   // this lane's 8 columns of its pair: stored only inside the valid width
-  // (with SPLIT the last chunk's first 4 columns only: col_hi false)
-  const bool col_ok = 32 * q + 8 * lg < NV;
-  const bool col_hi = 32 * q + 8 * lg + 8 <= NV;
+  // (with SPLIT the last chunk's first rem columns only)
+  const int rem = NV - (32 * q + 8 * lg);
+  const bool col_ok = rem > 0;
 
   // First product, one 16-row block of Z at a time: Z[rb] = X[rb] R[:, pair].
   constexpr int KSL = S::KSL;
@@ -460,9 +491,13 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     for (int ks = 0; ks < KS1; ++ks) {
       V a = *reinterpret_cast<const V*>(xs + ((rb * KS1 + ks) * 64 + lane) * 8);
       if (NV < S::N && ks == KS1 - 1 && 32 * ks + 8 * lg >= NV) a = V{};   // padded k
-      if (S::SPLIT && ks == KS1 - 1 && 32 * ks + 8 * lg + 4 == NV) {         // half-padded chunk
+      if (S::SPLIT && ks == KS1 - 1) {                                        // partly padded chunk
+        const int kv = NV - (32 * ks + 8 * lg);
+        if (kv > 0 && kv < 8) {
 #pragma unroll
-        for (int j = 4; j < 8; ++j) a[j] = DT::from_f(0.0f);
+          for (int j = 2; j < 8; ++j)
+            if (j >= kv) a[j] = DT::from_f(0.0f);
+        }
       }
       if (MV < S::M && rb == MB - 1 && 16 * rb + li >= MV) a = V{};        // padded row
       acc0 = Ops::mfma(a, rf[0][ks], acc0);
@@ -532,14 +567,11 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
 #pragma unroll
       for (int r = 0; r < 4; ++r) Epi::accumulate(word, yp[mb][r], rcp, r);
       if constexpr (S::SPLIT) {
-        // nibble offset t F + m NV + 8 (4q + lg) is a multiple of 4: two 16-bit
-        // halves; 16 rows further on is 4 NV halves further on
-        uint16_t* o16 = reinterpret_cast<uint16_t*>(out_codes) + t * (F / 4) + (li * NV + 32 * q + 8 * lg) / 4 +
-                        mb * (4 * NV);
-        if (col_ok && 16 * mb + li < MV) {
-          o16[0] = (uint16_t)word;
-          if (col_hi) o16[1] = (uint16_t)(word >> 16);
-        }
+        // nibble offset t F + m NV + 8 (4q + lg) is even: a byte offset; 16
+        // rows further on is 8 NV bytes further on
+        uint8_t* ob = reinterpret_cast<uint8_t*>(out_codes) + t * (F / 2) + (li * NV + 32 * q + 8 * lg) / 2 +
+                      mb * (8 * NV);
+        if (col_ok && 16 * mb + li < MV) fq_store_packed_split<NV>(ob, word, rem);
       } else {
         if (col_ok && 16 * mb + li < MV) orow[(16 * mb + li) * (NV / 8)] = (int32_t)word;
       }
@@ -569,11 +601,8 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
 #pragma unroll
       for (int j = 0; j < 8; ++j) word |= (uint32_t)(code[j] + 8) << (4 * j);
       if constexpr (S::SPLIT) {
-        uint16_t* o16 = reinterpret_cast<uint16_t*>(out_codes) + t * (F / 4) + (m * NV + 32 * q + 8 * lg) / 4;
-        if (col_ok) {
-          o16[0] = (uint16_t)word;
-          if (col_hi) o16[1] = (uint16_t)(word >> 16);
-        }
+        uint8_t* ob = reinterpret_cast<uint8_t*>(out_codes) + t * (F / 2) + (m * NV + 32 * q + 8 * lg) / 2;
+        if (col_ok) fq_store_packed_split<NV>(ob, word, rem);
       } else {
         if (col_ok) reinterpret_cast<int32_t*>(out_codes)[t * (F / 8) + m * (NV / 8) + 4 * q + lg] = (int32_t)word;
       }
@@ -585,11 +614,8 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
         hi4 |= (uint32_t)(code[4 + j] & 0xFF) << (8 * j);
       }
       int8_t* ob = reinterpret_cast<int8_t*>(out_codes) + t * F + m * NV + 32 * q + 8 * lg;
-      if constexpr (S::SPLIT) {   // 4-byte aligned
-        if (col_ok) {
-          *reinterpret_cast<int32_t*>(ob) = (int32_t)lo4;
-          if (col_hi) *reinterpret_cast<int32_t*>(ob + 4) = (int32_t)hi4;
-        }
+      if constexpr (S::SPLIT) {
+        if (col_ok) fq_store_int8_split<NV>(ob, lo4, hi4, rem);
       } else {
         v2i pair = {(int)lo4, (int)hi4};
         if (col_ok) *reinterpret_cast<v2i*>(ob) = pair;
@@ -1563,6 +1589,7 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE_NV(5, 4, 112)   // 80 x 112  (hidden 8960)
   QO_FQ_CASE_NV(8, 5, 148)   // 128 x 148 (hidden 18944; 16-bit code halves)
   QO_FQ_CASE_NV(8, 6, 172)   // 128 x 172 (hidden 22016; 16-bit code halves)
+  QO_FQ_CASE_NV(4, 7, 214)   // 64 x 214  (hidden 13696; byte code stores)
 #undef QO_FQ_CASE_NV
   // heights that are not a multiple of 16: computed zero-padded to 16 MB
 #define QO_FQ_CASE_MV(MB_, NP_, MV_)                                                                          \

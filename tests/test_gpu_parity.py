@@ -137,6 +137,9 @@ SHAPES = [
     (4, 128, 148, torch.float16, 1.0, False),    # the same, int8 codes in 4-byte pieces
     (3, 128, 172, torch.float16, 0.9, True),     # N = 172 (hidden 22016)
     (1100, 128, 148, torch.float16, 0.9, True),  # 8-byte aligned rows over many tokens
+    (5, 64, 214, torch.bfloat16, 0.9, True),     # N = 214 (hidden 13696): rows 4-byte aligned, byte code stores
+    (4, 64, 214, torch.float16, 1.0, False),     # the same, int8 codes in 16-bit pieces
+    (2000, 64, 214, torch.float16, 0.9, True),   # the same over many tokens
     (3, 144, 192, torch.bfloat16, 0.9, True),    # M = 144, odd M / 16 (hidden 27648)
     (4, 160, 160, torch.float16, 1.0, False),    # M = 160 (hidden 25600), int8 codes
     (900, 160, 160, torch.bfloat16, 0.9, True),  # 160 KB of LDS per group, over many tokens
@@ -158,7 +161,8 @@ def test_quantize_shapes(gpu, t, m, n, dtype, clip, pack):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mn", [(64, 64), (112, 128), (64, 96), (128, 224), (64, 80), (64, 112), (56, 64), (86, 128),
                                 (108, 128), (32, 48), (64, 88), (80, 112), (40, 64), (72, 96), (76, 128),
-                                (128, 148), (128, 172), (144, 192), (160, 160)])
+                                (128, 148), (128, 172), (144, 192), (160, 160),
+                                (64, 214)])
 def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
     m, n = mn
     case = wl.quant_case("xcheck", 37, m, n, dtype, 0.9, True, seed=5, outlier_frac=0.005, outlier_scale=30.0)
