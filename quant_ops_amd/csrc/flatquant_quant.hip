@@ -418,6 +418,12 @@ struct FqShape {
   static constexpr int FRAGS_PER_WAVE = STAGE_FRAGS / WAVES;   // == MB
   static constexpr int DMA_PER_WAVE = (SPLIT ? 4 : 1) * FRAGS_PER_WAVE;
   static constexpr int STAGE_ELEMS = STAGE_FRAGS * 512;
+  // One X stage instead of two where two would not fit in LDS beside L's
+  // fragments: the next group's copy is then issued once every wave's first
+  // product has read the stage (it still overlaps the second product and the
+  // epilogue).
+  static constexpr int LF_BYTES = LF_LDS ? LF_FRAGS * 1024 : 16;
+  static constexpr bool ONE_STAGE = 2 * STAGE_ELEMS * 2 + LF_BYTES + 8 * TPB * NP > 160 * 1024;
   static_assert(STAGE_FRAGS % WAVES == 0, "X fragments must split evenly over waves");
   static_assert(M * M <= STAGE_ELEMS, "L must fit in one X stage while it is staged");
   static_assert(DMA_PER_WAVE < 64, "vmcnt range");
@@ -463,13 +469,14 @@ __device__ inline void fq_store_int8_split(int8_t* o, uint32_t lo4, uint32_t hi4
 
 // One token group (this wave's token slot and pair) from an X stage in LDS:
 // both products, the per-token scale and the codes.
-template <class DT, int MB, int NP, bool PACK, int NV, int MV>
+// after_x() runs once the first product has read the X stage.
+template <class DT, int MB, int NP, bool PACK, int NV, int MV, class AfterX>
 __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FqShape<MB, NP>::KS2 + 1],
     const unsigned char* lf_lds,
     const typename MfmaOps<DT>::V (&rf)[2][FqShape<MB, NP>::KS1], float (*red)[NP][2], int64_t t,
     int64_t tokens, float clip, void* __restrict__ out_codes, float* __restrict__ out_scales, int lane,
-    int tau, int q) {
+    int tau, int q, AfterX&& after_x) {
   using S = FqShape<MB, NP, NV, MV>;
   using T = typename DT::T;
   using Ops = MfmaOps<DT>;
@@ -517,6 +524,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     // (their VGPRs would not fit next to L's and R's fragments)
     __builtin_amdgcn_sched_barrier(0);
   }
+  after_x();
 
   // Second product, transposed: Y^T[n][m] = sum_m' Z[m'][n] L[m'][m].
   using Epi = FqEpi<DT>;
@@ -636,9 +644,11 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   constexpr int NT = S::WAVES * 64;
 
   // Two X stages as distinct objects: the compiler then knows that reading one
-  // stage does not depend on the LDS-DMA still writing the other.
+  // stage does not depend on the LDS-DMA still writing the other. L is staged
+  // through the stage that is free at set-up.
   __shared__ __align__(16) T xbuf0[S::STAGE_ELEMS];
-  __shared__ __align__(16) T xbuf1[S::STAGE_ELEMS];
+  __shared__ __align__(16) T xbuf1[S::ONE_STAGE ? 8 : S::STAGE_ELEMS];
+  T* const lstage = S::ONE_STAGE ? xbuf0 : xbuf1;
   __shared__ __align__(16) unsigned char lf_lds[S::LF_LDS ? S::LF_FRAGS * 1024 : 16];
   __shared__ float red[S::TPB][NP][2];
 
@@ -701,7 +711,9 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   };
 
   int64_t g = blockIdx.x;
-  issue(g, xbuf0);   // first X group in flight while L and R are set up (grid <= ngroups)
+  // first X group in flight while L and R are set up (grid <= ngroups); with
+  // one stage, once L has been staged through it
+  if constexpr (!S::ONE_STAGE) issue(g, xbuf0);
 
   // R as B-operand fragments of the first product for this wave's pair:
   // rf[h][ks][j] = R[32ks + 8lg + j][n], n = 32q + 8(li/4) + 4h + li%4.
@@ -738,13 +750,13 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 #pragma unroll
     for (int i = 0; i < (CHUNKS + NT - 1) / NT; ++i) {
       const int c = tid + i * NT;
-      if (c < CHUNKS) reinterpret_cast<v4i_t*>(xbuf1)[c] = tmp[i];
+      if (c < CHUNKS) reinterpret_cast<v4i_t*>(lstage)[c] = tmp[i];
     }
-    if (TAILE > 0 && tid < TAILE) xbuf1[8 * CHUNKS + tid] = left[8 * CHUNKS + tid];
+    if (TAILE > 0 && tid < TAILE) lstage[8 * CHUNKS + tid] = left[8 * CHUNKS + tid];
   }
   lds_barrier();
   // L[m'][m] of the staged MV x MV rows, 0 in the padding
-  auto lval = [&](int mp, int m) { return (mp < MV && m < MV) ? xbuf1[mp * MV + m] : DT::from_f(0.0f); };
+  auto lval = [&](int mp, int m) { return (mp < MV && m < MV) ? lstage[mp * MV + m] : DT::from_f(0.0f); };
   V lf[MB][KS2 + 1];
   auto lfrag = [&](int mb, int s) {   // fragment (mb, s); s = KS2 is the zero-padded trailing slab
     V v;
@@ -765,20 +777,35 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 #pragma unroll
       for (int s = 0; s <= KS2; ++s) lf[mb][s] = lfrag(mb, s);
   }
-  lds_barrier();   // xbuf1 is free again for the first prefetch
+  lds_barrier();   // the staging stage is free again for the first prefetch
 
-  while (g < ngroups) {
-    int64_t gn = g + gridDim.x;
-    prefetch_and_wait(gn, xbuf1);
-    fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf0 + tau * S::XFRAGS * 512, lf, lf_lds, rf, red, g * S::TPB + tau, tokens, clip,
-                                    out_codes, out_scales, lane, tau, q);
-    g = gn;
-    if (g >= ngroups) break;
-    gn = g + gridDim.x;
-    prefetch_and_wait(gn, xbuf0);
-    fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf1 + tau * S::XFRAGS * 512, lf, lf_lds, rf, red, g * S::TPB + tau, tokens, clip,
-                                    out_codes, out_scales, lane, tau, q);
-    g = gn;
+  if constexpr (S::ONE_STAGE) {
+    issue(g, xbuf0);
+    while (g < ngroups) {
+      const int64_t gn = g + gridDim.x;
+      wait_vmcnt<0>();
+      raw_barrier();
+      fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf0 + tau * S::XFRAGS * 512, lf, lf_lds, rf, red, g * S::TPB + tau,
+                                              tokens, clip, out_codes, out_scales, lane, tau, q, [&] {
+                                                lds_barrier();   // every wave's first product has read the stage
+                                                if (gn < ngroups) issue(gn, xbuf0);
+                                              });
+      g = gn;
+    }
+  } else {
+    while (g < ngroups) {
+      int64_t gn = g + gridDim.x;
+      prefetch_and_wait(gn, xbuf1);
+      fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf0 + tau * S::XFRAGS * 512, lf, lf_lds, rf, red, g * S::TPB + tau,
+                                              tokens, clip, out_codes, out_scales, lane, tau, q, [] {});
+      g = gn;
+      if (g >= ngroups) break;
+      gn = g + gridDim.x;
+      prefetch_and_wait(gn, xbuf0);
+      fq_mfma_group<DT, MB, NP, PACK, NV, MV>(xbuf1 + tau * S::XFRAGS * 512, lf, lf_lds, rf, red, g * S::TPB + tau,
+                                              tokens, clip, out_codes, out_scales, lane, tau, q, [] {});
+      g = gn;
+    }
   }
   wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
 }
@@ -1461,7 +1488,8 @@ static int launch_mfma(const void* x, int64_t tokens, int64_t x_ld, const void* 
                        float clip, void* out_codes, float* out_scales, hipStream_t stream) {
   using S = FqShape<MB, NP, NV, MV>;
   using T = typename DT::T;
-  constexpr size_t lds = 2 * S::STAGE_ELEMS * sizeof(T);  // static LDS of the kernel
+  // static LDS of the kernel (X stages; L's fragments counted where one stage is used)
+  constexpr size_t lds = S::ONE_STAGE ? S::STAGE_ELEMS * sizeof(T) + S::LF_BYTES : 2 * S::STAGE_ELEMS * sizeof(T);
   const int per_cu = (int)std::min<size_t>(4, (160 * 1024) / (lds + 256));
   const int64_t ngroups = (tokens + S::TPB - 1) / S::TPB;
   int64_t grid = (int64_t)device_cu_count() * per_cu;
@@ -1575,6 +1603,7 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE(8, 7)   // 128 x 224  (hidden 28672)
   QO_FQ_CASE(9, 6)   // 144 x 192  (hidden 27648)
   QO_FQ_CASE(10, 5)  // 160 x 160  (hidden 25600)
+  QO_FQ_CASE(8, 8)   // 128 x 256  (hidden 32768; one X stage)
 #undef QO_FQ_CASE
   // widths that are not a multiple of 32: computed zero-padded to 32 NP
 #define QO_FQ_CASE_NV(MB_, NP_, NV_)                                                                     \
@@ -1602,6 +1631,9 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   QO_FQ_CASE_MV(3, 2, 40)    // 40 x 64   (hidden 2560)
   QO_FQ_CASE_MV(5, 3, 72)    // 72 x 96   (hidden 6912)
   QO_FQ_CASE_MV(5, 4, 76)    // 76 x 128  (hidden 9728)
+  // both padded, one X stage
+  if (M == 168 && N == 176)   // 168 x 176 (hidden 29568)
+    return launch_mfma<DT, 11, 6, PACK, 176, 168>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream);
 #undef QO_FQ_CASE_MV
   *handled = false;
   return QO_OK;

@@ -141,6 +141,11 @@ SHAPES = [
     (4, 64, 214, torch.float16, 1.0, False),     # the same, int8 codes in 16-bit pieces
     (2000, 64, 214, torch.float16, 0.9, True),   # the same over many tokens
     (3, 144, 192, torch.bfloat16, 0.9, True),    # M = 144, odd M / 16 (hidden 27648)
+    (3, 128, 256, torch.bfloat16, 0.9, True),    # N = 256 (hidden 32768): one X stage
+    (2, 168, 176, torch.float16, 1.0, False),    # both padded, one X stage (hidden 29568), int8 codes
+    (3, 168, 176, torch.bfloat16, 0.9, True),    # the same, packed
+    (800, 128, 256, torch.float16, 0.9, True),   # one X stage, groups loop over many tokens
+    (700, 168, 176, torch.bfloat16, 1.0, True),  # the same
     (4, 160, 160, torch.float16, 1.0, False),    # M = 160 (hidden 25600), int8 codes
     (900, 160, 160, torch.bfloat16, 0.9, True),  # 160 KB of LDS per group, over many tokens
     (3000, 64, 80, torch.bfloat16, 0.9, True),   # padded width, groups loop over many tokens
@@ -162,7 +167,7 @@ def test_quantize_shapes(gpu, t, m, n, dtype, clip, pack):
 @pytest.mark.parametrize("mn", [(64, 64), (112, 128), (64, 96), (128, 224), (64, 80), (64, 112), (56, 64), (86, 128),
                                 (108, 128), (32, 48), (64, 88), (80, 112), (40, 64), (72, 96), (76, 128),
                                 (128, 148), (128, 172), (144, 192), (160, 160),
-                                (64, 214)])
+                                (64, 214), (128, 256), (168, 176)])
 def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
     m, n = mn
     case = wl.quant_case("xcheck", 37, m, n, dtype, 0.9, True, seed=5, outlier_frac=0.005, outlier_scale=30.0)
