@@ -1558,7 +1558,8 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   // token per group of 2-4 waves) finishes sooner than the one-wave and pair
   // kernels, whose per-token chain is longer; measured crossovers: 64 x 64
   // after 512 tokens (16 tokens bf16: 5.2 vs 6.4 us), 32 x 64 and 64 x 128
-  // after 256. Wider pair-kernel shapes keep the pair kernel at any count.
+  // after 256; 96 x 128 at up to 256 tokens too (1 token bf16: 6.8 vs 7.7 us).
+  // 112 x 128 and 128 x 128 keep the pair kernel at any count.
   const bool few = fq_route_few() && tokens <= (M == 64 && N == 64 ? 512 : 256);
   // the wave kernel takes the scale from max |Y|, which needs clip > 0
   if (fq_allow_wave() && clip > 0.f && clip <= 3.4e38f && !few) {
@@ -1573,7 +1574,7 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
 #undef QO_FQ_WAVE_CASE
   }
   // the pair kernel takes its scale from max |Y| as well
-  if (fq_allow_duo() && clip > 0.f && clip <= 3.4e38f && N == 128 && !(few && M == 64)) {
+  if (fq_allow_duo() && clip > 0.f && clip <= 3.4e38f && N == 128 && !(few && (M == 64 || M == 96))) {
 #define QO_FQ_DUO_CASE(MB_)                                                                                  \
     if (M == 16 * (MB_))                                                                                     \
       return launch_duo<DT, MB_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream);
