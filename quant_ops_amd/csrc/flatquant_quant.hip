@@ -382,6 +382,24 @@ struct FqEpi<BF16T> {
   __device__ static inline uint32_t amax_bits(const Amax& a) { return max(a.m & 0xFFFFu, a.m >> 16); }
 };
 
+// LDS transpose read of 16-bit elements (gfx950 ds_read_b64_tr_b16): within
+// each 16-lane group, lane l supplies the address of 4 consecutive elements
+// (8-byte aligned), forming row l of a 16 x 4 matrix A; lane i receives
+// A[i/4][i%4], A[4 + i/4][i%4], A[8 + i/4][i%4], A[12 + i/4][i%4] — that is,
+// A[4e + i/4][i%4] for e = 0..3 (checked on the device).
+typedef short v4s16 __attribute__((ext_vector_type(4)));
+__device__ inline v4s16 lds_tr16(const void* p) {
+  typedef __attribute__((address_space(3))) v4s16* lds_v4s16;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s16)(__attribute__((address_space(3))) const void*)p);
+}
+// Two 4-element reads as one 8-element MFMA operand (elements 0..3, 4..7).
+template <class V>
+__device__ inline V join_tr16(v4s16 lo, v4s16 hi) {
+  typedef short v8s16 __attribute__((ext_vector_type(8)));
+  const v8s16 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(V, w);
+}
+
 // NV, MV: the token's width and height in memory; N = 32 NP and M = 16 MB are
 // computed, the rest is zero padding (X's padded columns and rows zeroed in
 // registers, R's and L's padded rows and columns zero, padded codes not
@@ -759,12 +777,22 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
   auto lval = [&](int mp, int m) { return (mp < MV && m < MV) ? lstage[mp * MV + m] : DT::from_f(0.0f); };
   V lf[MB][KS2 + 1];
   auto lfrag = [&](int mb, int s) {   // fragment (mb, s); s = KS2 is the zero-padded trailing slab
-    V v;
+    if constexpr (MV == S::M && !S::LF_LDS) {
+      // unpadded L held in VGPRs: two LDS transpose reads (lds_tr16) of 4 consecutive rows of
+      // column 16mb + li, rows 32s + 4lg .. +3 (elements 0..3) and 16 rows on (4..7);
+      // lane li supplies the address of row 32s + 4lg + li/4, columns 16mb + 4(li%4) .. +3
+      const T* at = lstage + (32 * s + 4 * lg + (li >> 2)) * MV + 16 * mb + 4 * (li & 3);
+      if (s < KS2) return join_tr16<V>(lds_tr16(at), lds_tr16(at + 16 * MV));
+      if (S::TAIL) return join_tr16<V>(lds_tr16(at), v4s16{0, 0, 0, 0});
+      return V{};
+    } else {
+      V v;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      v[j] = s < KS2 ? lval(32 * s + 16 * (j >> 2) + 4 * lg + (j & 3), 16 * mb + li)
-                     : (S::TAIL && j < 4) ? lval(16 * (MB - 1) + 4 * lg + j, 16 * mb + li) : DT::from_f(0.0f);
-    return v;
+      for (int j = 0; j < 8; ++j)
+        v[j] = s < KS2 ? lval(32 * s + 16 * (j >> 2) + 4 * lg + (j & 3), 16 * mb + li)
+                       : (S::TAIL && j < 4) ? lval(16 * (MB - 1) + 4 * lg + j, 16 * mb + li) : DT::from_f(0.0f);
+      return v;
+    }
   };
   if constexpr (S::LF_LDS) {
     // the waves split the fragments; the barrier below makes them visible
@@ -834,23 +862,6 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 // routes clip <= 0 elsewhere.
 // ---------------------------------------------------------------------------
 
-// LDS transpose read of 16-bit elements (gfx950 ds_read_b64_tr_b16): within
-// each 16-lane group, lane l supplies the address of 4 consecutive elements
-// (8-byte aligned), forming row l of a 16 x 4 matrix A; lane i receives
-// A[i/4][i%4], A[4 + i/4][i%4], A[8 + i/4][i%4], A[12 + i/4][i%4] — that is,
-// A[4e + i/4][i%4] for e = 0..3 (checked on the device).
-typedef short v4s16 __attribute__((ext_vector_type(4)));
-__device__ inline v4s16 lds_tr16(const void* p) {
-  typedef __attribute__((address_space(3))) v4s16* lds_v4s16;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s16)(__attribute__((address_space(3))) const void*)p);
-}
-// Two 4-element reads as one 8-element MFMA operand (elements 0..3, 4..7).
-template <class V>
-__device__ inline V join_tr16(v4s16 lo, v4s16 hi) {
-  typedef short v8s16 __attribute__((ext_vector_type(8)));
-  const v8s16 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(V, w);
-}
 
 template <class DT>
 struct DBits;
