@@ -6,14 +6,18 @@
 // (flatquant/kernels/cuda_quant_kernel.cu:231-390) and follows the rounding
 // points of its PyTorch fallback (flatquant/ops.py:99-130).
 //
-// Two kernels:
-//  * fq_mfma_kernel   — D in {fp16, bf16}, M % 16 == 0 (M <= 128), N = 32 NP (listed shapes).
+// Kernels:
+//  * fq_wave_kernel   — one wave per token, M, N <= 64 (fp16 / bf16).
+//  * fq_duo_kernel    — a pair of waves per token, N = 128, M in {64, 96, 112, 128}.
+//  * fq_mfma_kernel   — D in {fp16, bf16}, the listed shapes: M up to 176 zero-padded
+//                       to 16 MB, N even up to 256 zero-padded to 32 NP.
 //                       Both contractions on v_mfma_f32_16x16x32_{f16,bf16}; X is
-//                       streamed into LDS by LDS-DMA (global_load_lds_dwordx4)
-//                       one token group ahead; L is resident in LDS, R in VGPRs.
+//                       streamed into LDS by LDS-DMA one token group ahead (two
+//                       stages, one where two do not fit); L is resident in VGPRs
+//                       or LDS, R in VGPRs.
 //  * fq_generic_kernel — any M, N, D in {fp32, fp16, bf16}; VALU fp32 FMA with the
-//                       same rounding points. Used for shapes the MFMA kernel
-//                       does not cover (and for fp32 inputs).
+//                       same rounding points. Used for shapes the MFMA kernels
+//                       do not cover (and for fp32 inputs).
 #include <stdarg.h>
 #include <stdio.h>
 
