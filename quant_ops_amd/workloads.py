@@ -20,10 +20,28 @@ import torch
 
 
 def orthogonal(n: int, seed: int, dtype=torch.float32) -> torch.Tensor:
-    """Q of the QR factorisation of a seeded N(0, 1) n x n matrix, cast to ``dtype``."""
+    """Q of the QR factorisation of a seeded N(0, 1) n x n matrix, cast to ``dtype``.
+
+    The factorisation runs in float64: LAPACK builds on different host CPUs
+    return float32 Q factors that differ in the last bits, which after the cast
+    to fp16 changed 26 of 4096 entries of a 64 x 64 Q between this container
+    and a GPU box host. In float64 those differences are far below the rounding
+    of the cast, so every host builds the same transforms.
+    """
     g = torch.Generator().manual_seed(seed)
-    q, _ = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float32))
+    a = torch.randn(n, n, generator=g, dtype=torch.float32).double()
+    q, _ = torch.linalg.qr(a)
     return q.to(dtype).contiguous()      # QR returns Q column-major
+
+
+def gaussian_transforms(m: int, n: int, dtype, seed: int):
+    """Non-orthogonal N(0, 1) transforms L [m, m] and R [n, n] in ``dtype``, as the
+    reference's own tests build them (tests/test_performance.py:28-37,
+    tests/test_accuracy.py:38-40)."""
+    g = torch.Generator().manual_seed(seed)
+    left = torch.randn(m, m, generator=g, dtype=torch.float32).to(dtype)
+    right = torch.randn(n, n, generator=g, dtype=torch.float32).to(dtype)
+    return left, right
 
 
 def activations(tokens: int, features: int, dtype, seed: int, outlier_frac: float = 0.0,
@@ -83,6 +101,20 @@ def quant_case(name: str, tokens: int, m: int, n: int, dtype, clip: float, pack:
                outlier_frac: float = 0.0, outlier_scale: float = 1.0) -> QuantCase:
     x = activations(tokens, m * n, dtype, seed, outlier_frac, outlier_scale)
     return QuantCase(name, x, orthogonal(m, seed + 1, dtype), orthogonal(n, seed + 2, dtype), clip, pack)
+
+
+def reference_test_case(tokens: int, features: int, dtype, clip: float = 1.0, pack: bool = False,
+                        seed: int = 42) -> QuantCase:
+    """The reference tests' inputs: X ~ N(0, 1) [tokens, features] in ``dtype``, the
+    Kronecker dims from ``get_decompose_dim`` and N(0, 1) (non-orthogonal) L and R
+    in ``dtype`` (tests/test_performance.py:28-37,215-251)."""
+    from .decompose import get_decompose_dim
+
+    m, n = get_decompose_dim(features)
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(tokens, features, generator=g, dtype=torch.float32).to(dtype)
+    left, right = gaussian_transforms(m, n, dtype, seed + 1)
+    return QuantCase(f"ref_{tokens}x{features}_{str(dtype)[6:]}_{m}x{n}", x, left, right, clip, pack)
 
 
 def quant_cfg1(tokens: int = 128, seed: int = 0) -> QuantCase:

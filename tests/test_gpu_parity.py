@@ -45,10 +45,10 @@ def _ulps(a, b, dtype):
 def check_quant(x, L, R, clip, pack, q_gpu, s_gpu, tag):
     """Compare kernel output with the oracle; returns (flip fraction, scale bit-equal fraction).
 
-    Scales: the bar is 1e-3 relative. A token's scale can only differ when the
-    kernel's and the CPU BLAS's float32 accumulation orders round that token's
-    absmax element of Y differently (one D ulp, which is 2^-8..2^-7 relative in
-    bf16); such tokens must stay rare (<= 1 %) and within 2 ulps of D.
+    Scales: every token within 1e-3 relative (for bf16, whose ulp is
+    2^-8..2^-7 relative, that means bit-equal). A token's scale can only differ
+    where the kernel's and the host BLAS's float32 summation orders round that
+    token's absmax element of Y to different neighbours of D.
     """
     q_ref, s_ref = ofq.flatquant_pytorch(x, L, R, clip, pack)
     s_ref32 = s_ref.float()
@@ -58,8 +58,9 @@ def check_quant(x, L, R, clip, pack, q_gpu, s_gpu, tag):
     srel = torch.where(s_g == s_ref32, torch.zeros_like(s_ref32), (s_g - s_ref32).abs() / denom)
     ulps = _ulps(s_g, s_ref32, x.dtype)
     over = float((srel > SCALE_RTOL).float().mean())
-    assert int(ulps.max()) <= 2, f"{tag}: scale differs by {int(ulps.max())} ulps"
-    assert over <= 0.01, f"{tag}: {over:.3%} of scales beyond {SCALE_RTOL} relative"
+    assert float(srel.max()) <= SCALE_RTOL, (
+        f"{tag}: {over:.3%} of scales beyond {SCALE_RTOL} relative (max {float(srel.max()):.2e}, "
+        f"{int(ulps.max())} ulp)")
     qg = _codes_int8(q_gpu, pack).to(torch.int16)
     qr = _codes_int8(q_ref, pack).to(torch.int16)
     assert qg.shape == qr.shape
@@ -93,8 +94,44 @@ def test_quantize_baseline_configs(gpu, cfg):
     _say(f"{case.name}: T={case.tokens} F={case.features} {case.x.dtype} pack={case.pack_int32}")
     q, s = run_capi_quant(case, gpu)
     flips, same = check_quant(case.x, case.left, case.right, case.clip_ratio, case.pack_int32, q, s, case.name)
-    # the kernel rounds where the fallback rounds: flips stay far below the bar
-    assert flips <= 2e-4 and same >= 0.95
+    # the kernel rounds where the fallback rounds: flips stay far below the bar and
+    # scales are bit-equal but where a summation order flips a token's absmax
+    assert flips <= 2e-4 and same >= 0.99
+
+
+# The reference tests' own inputs (tests/test_accuracy.py:30-40,
+# tests/test_performance.py:28-37,215-251): X and non-orthogonal L, R all
+# N(0, 1) in the input dtype, Kronecker dims from get_decompose_dim, clip 1.0.
+# With Gaussian transforms |Y| is about sqrt(M N) = 64 times larger than with
+# orthogonal ones.
+REFERENCE_INPUTS = [
+    (128, 4096, torch.float16),
+    (64, 2048, torch.float16),
+    (256, 4096, torch.float32),
+    (512, 4096, torch.bfloat16),
+    (256, 4096, torch.float16),
+    (512, 4096, torch.float16),
+    (1024, 4096, torch.float16),
+    (256, 4096, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("pack", [False, True])
+@pytest.mark.parametrize("t,f,dtype", REFERENCE_INPUTS)
+def test_quantize_reference_test_inputs(gpu, t, f, dtype, pack):
+    case = wl.reference_test_case(t, f, dtype, 1.0, pack)
+    _say(f"{case.name} pack={pack}")
+    q, s = run_capi_quant(case, gpu)
+    check_quant(case.x, case.left, case.right, 1.0, pack, q, s, f"{case.name} pack={pack}")
+    # the reference's packing test (tests/test_accuracy.py:90-120): packed and
+    # int8 codes of the same call dequantize to the same values
+    x, L, R = case.x.to(gpu), case.left.to(gpu), case.right.to(gpu)
+    q_other, s_other = qo.flatquant_dynamic_quantize(x, L, R, 1.0, not pack)
+    torch.cuda.synchronize()
+    assert torch.equal(s_other.cpu(), s.cpu())
+    d1 = qo.dequantize_int4(q, s, pack)
+    d2 = qo.dequantize_int4(q_other, s_other, not pack)
+    assert torch.equal(d1, d2)
 
 
 SHAPES = [
@@ -229,7 +266,7 @@ def test_quantize_matches_sequential_accumulation_oracle(gpu, dtype, mn, monkeyp
     the generic kernel is bit-exact, the MFMA kernel differs only where its
     internal summation order rounds Z or Y differently."""
     m, n = mn
-    case = wl.quant_case("seq", 96, m, n, dtype, 0.9, True, seed=17, outlier_frac=0.01, outlier_scale=20.0)
+    case = wl.quant_case("seq", 512, m, n, dtype, 0.9, True, seed=17, outlier_frac=0.01, outlier_scale=20.0)
     q_ref, s_ref = ofq.flatquant_sequential(case.x, case.left, case.right, 0.9, True)
     monkeypatch.setenv("QO_FQ_FORCE_GENERIC", "1")
     qg, sg = run_capi_quant(case, gpu)
@@ -240,7 +277,9 @@ def test_quantize_matches_sequential_accumulation_oracle(gpu, dtype, mn, monkeyp
     d = (_codes_int8(qm, True).int() - _codes_int8(q_ref, True).int()).abs()
     same = float((sm.cpu() == s_ref.float()).float().mean())
     _say(f"  mfma: flips {float((d != 0).float().mean()):.2e}, scales bit-equal {same:.4f}")
-    assert int(d.max()) <= 1 and float((d != 0).float().mean()) <= 1e-4 and same >= 0.97
+    srel = ((sm.cpu() - s_ref.float()).abs() / s_ref.float().abs()).max()
+    assert int(d.max()) <= 1 and float((d != 0).float().mean()) <= 1e-4
+    assert float(srel) <= SCALE_RTOL and same >= 0.99
 
 
 @pytest.mark.parametrize("pack", [True, False])
