@@ -232,3 +232,64 @@ def test_workload_generators_are_seeded():
     g = wl.gemm_case(32, 48, 64, b_transposed_view=True)
     assert g.b.shape == (8, 48) and g.b.stride() == (1, 8)
     assert wl.gemm_cfg4().ops() == 481_036_337_152
+
+
+# ----------------------------------------------------------------- the reference's import surface
+
+def test_reference_import_paths_resolve():
+    """Every name the reference's examples and tests import resolves to this
+    build's object (examples/basic_usage.py:13-14, examples/int4_matmul_benchmark.py:12-13,
+    tests/test_accuracy.py:15-20, tests/test_performance.py:21-26)."""
+    import quant_ops
+    import quant_ops_amd
+    from quant_ops import (CUDA_AVAILABLE, dequantize_int4, flatquant_dynamic_quantize, get_decompose_dim,
+                           int4_matmul)
+    from quant_ops.ops.quantization.flatquant.ops import flatquant_cuda, flatquant_pytorch
+    from quant_ops.ops.quantization.flatquant.kernels import CUDA_KERNELS_AVAILABLE as FQ_AVAILABLE
+    from quant_ops.ops.quantization.flatquant.kernels import cuda_quant_ops
+    from quant_ops.ops.quantization.int4_matmul.ops import int4_matmul_cuda, int4_matmul_pytorch, pack_int4_to_int32
+    from quant_ops.ops.quantization.int4_matmul.ops import unpack_int32_to_int4
+    from quant_ops.ops.quantization.int4_matmul.kernels import CUDA_KERNELS_AVAILABLE as MM_AVAILABLE
+    from quant_ops.ops.quantization.int4_matmul.kernels import cuda_int4_matmul_ops
+    from quant_ops.ops.quantization.int4_matmul import int4_matmul as int4_matmul_pkg
+    from quant_ops.ops.quantization.flatquant import flatquant_dynamic_quantize as fdq_pkg
+    from quant_ops.utils.decompose import get_decompose_dim as gdd
+    from quant_ops.utils import get_decompose_dim as gdd2
+    import quant_ops.meta_ops  # noqa: F401
+
+    assert quant_ops.__version__ == quant_ops_amd.__version__
+    assert sorted(quant_ops.__all__) == sorted(["flatquant_dynamic_quantize", "dequantize_int4", "int4_matmul",
+                                                "get_decompose_dim", "CUDA_AVAILABLE"])
+    assert flatquant_dynamic_quantize is quant_ops_amd.flatquant_dynamic_quantize is fdq_pkg
+    assert dequantize_int4 is quant_ops_amd.dequantize_int4
+    assert int4_matmul is quant_ops_amd.int4_matmul is int4_matmul_pkg
+    assert get_decompose_dim is gdd is gdd2 is quant_ops_amd.get_decompose_dim
+    assert flatquant_cuda is quant_ops_amd.flatquant_cuda and flatquant_pytorch is quant_ops_amd.flatquant_pytorch
+    assert int4_matmul_cuda is quant_ops_amd.int4_matmul_cuda
+    assert int4_matmul_pytorch is quant_ops_amd.int4_matmul_pytorch
+    assert pack_int4_to_int32 is quant_ops_amd.pack_int4_to_int32
+    assert unpack_int32_to_int4 is quant_ops_amd.unpack_int32_to_int4
+    assert CUDA_AVAILABLE == quant_ops_amd.CUDA_AVAILABLE == FQ_AVAILABLE == MM_AVAILABLE
+    if CUDA_AVAILABLE:
+        assert callable(cuda_quant_ops.cuda_kronecker_quant_int8)
+        assert callable(cuda_int4_matmul_ops.cuda_int4_matmul)
+    else:
+        assert cuda_quant_ops is None and cuda_int4_matmul_ops is None
+    # the reference's CPU path through the new import surface
+    x = torch.randn(4, 4096, dtype=torch.float16)
+    L = torch.eye(64, dtype=torch.float16)
+    q, s = flatquant_dynamic_quantize(x, L, L, 1.0, True, use_cuda=False)
+    assert q.shape == (4, 512) and s.shape == (4,)
+
+
+def test_pybind_equivalents_check_arguments_like_the_reference():
+    """cuda_int4_matmul rejects host tensors and non-float32 scales with the
+    reference's messages (cuda_int4_matmul_kernel.cu:136-150)."""
+    from quant_ops_amd import extension
+
+    if not extension.CUDA_KERNELS_AVAILABLE:
+        pytest.skip("HIP library not built")
+    a = torch.zeros(2, 1, dtype=torch.int32)
+    b = torch.zeros(1, 3, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="a_packed must be on CUDA"):
+        extension.cuda_int4_matmul(a, b, torch.ones(2), torch.ones(3))

@@ -358,6 +358,29 @@ def test_quantize_torch_op_matches_capi_and_stream(gpu):
     assert s4.dtype == torch.float16
 
 
+def test_pybind_equivalents_match_the_operators(gpu):
+    """cuda_kronecker_quant_int8 / cuda_int4_matmul, reached through the
+    reference's module paths, give the operators' results; host inputs are
+    moved to the GPU by the quantize entry as the reference's does."""
+    from quant_ops.ops.quantization.flatquant.kernels import cuda_quant_ops
+    from quant_ops.ops.quantization.int4_matmul.kernels import cuda_int4_matmul_ops
+
+    case = wl.quant_cfg2(tokens=96, seed=8)
+    x, L, R = case.x.to(gpu), case.left.to(gpu), case.right.to(gpu)
+    q1, s1 = qo.flatquant_dynamic_quantize(x, L, R, 0.9, True)
+    q2, s2 = cuda_quant_ops.cuda_kronecker_quant_int8(case.x, case.left, case.right, 0.9, True)
+    torch.cuda.synchronize()
+    assert q2.is_cuda and torch.equal(q1, q2) and torch.equal(s1, s2)
+    g = wl.gemm_case(64, 128, 256, seed=9)
+    a, b = g.a.to(gpu), g.b.to(gpu)
+    sa, sb = g.scale_a.float().to(gpu), g.scale_b.float().to(gpu)
+    out = cuda_int4_matmul_ops.cuda_int4_matmul(a, b, sa, sb)
+    torch.cuda.synchronize()
+    assert torch.equal(out, qo.int4_matmul(a, b, sa, sb))
+    with pytest.raises(RuntimeError, match="scale_a must be float32"):
+        cuda_int4_matmul_ops.cuda_int4_matmul(a, b, sa.half(), sb)
+
+
 def test_quantize_graph_capture_replays(gpu):
     case = wl.quant_cfg2(tokens=256, seed=4)
     x, L, R = case.x.to(gpu), case.left.to(gpu), case.right.to(gpu)
