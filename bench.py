@@ -1,20 +1,36 @@
 #!/usr/bin/env python3
 """Benchmark of the FlatQuant W4A4 hot path on one MI355X.
 
-Prints ONE JSON line. The primary workload (``value``) is BASELINE config 2:
-the fused quantize of fp16 X [2048, 4096] with 64 x 64 orthogonal transforms,
-clip 0.9, packed int32 codes — one "step" is one quantize call over that batch.
-``value`` is algorithmic HBM bytes (X in + codes out + fp32 scales + L, R) per
-second over exactly ``--steps`` back-to-back steps (a captured HIP graph,
-inputs already in HBM, rotated over enough buffers to exceed the 256 MB MALL),
-timed with HIP events on the stream the kernels run on.
+Prints ONE JSON line. The headline (``value``) is BASELINE config 4, the W4A4
+GEMM 4096 x 14336 x 4096 the north-star target names: int32-packed int4 codes
+times int32-packed int4 codes on the i8 MFMA with int32 accumulation, fp16
+per-token and per-channel scales, fp16 output. One step is one GEMM call;
+``value`` is 2 M N K per step over the time of exactly ``--steps`` steps.
 
-Secondary objects carry the W4A4 GEMM (config 4, TOPS vs the int8 MFMA peak),
-the wide quantize (config 3) and the end-to-end W4A4 linear (config 5).
-``cpu_baseline`` times this repo's CPU restatement of the reference PyTorch
-fallback on a bounded sample on the host cores (a reported baseline, not a target).
+Every BASELINE config has an object in ``lines`` with its own ``roofline``
+(achieved rate of the config's dominant kernel against the MI355X peak of its
+bound) and ``cpu_baseline`` (this repo's CPU restatement of the reference
+fallback, timed on the host cores on a bounded sample, in the same unit):
 
-Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--warm-s 0.2] [--no-secondary] [--no-cpu]
+* ``gemm_cfg4`` (the headline), ``quantize_cfg2``, ``quantize_cfg3``;
+* ``linear_cfg5_T16`` and ``linear_cfg5_T4096``: quantize + GEMM as one step,
+  and each kernel timed alone; T = 16 is judged on the HBM rate of the GEMM,
+  whose bytes are the 29.4 MB weight read;
+* ``quantize_cfg1``: the fp32 CPU-plumbing config, with the round-trip errors
+  of ``dequantize_int4`` for the CPU fallback and for the GPU kernel.
+
+Beside them: ``copy_probe_cfg2_bytes`` (a plain elementwise copy moving config
+2's byte count, the launch + streaming floor that quantize is compared with),
+``layout_cfg4_weight`` and ``dequant_cfg2``.
+
+Timing: inputs already in HBM. Each measurement captures ``--steps`` launches in
+one HIP graph, replays it untimed (at least ``--warm-s`` seconds), then replays
+it once between two HIP events recorded on the stream that launches it. Every
+step has its own buffer set (inputs and outputs) while the sets fit in 48 GiB,
+and there are always enough sets to exceed 1.25 x the 256 MB MALL, so a timed
+step never finds its inputs left in the MALL by an earlier step.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--warm-s 0.2] [--no-secondary] [--no-cpu]
        python bench.py --pmc-pass                       (under rocprofv3 --pmc FETCH_SIZE or WRITE_SIZE)
        python bench.py --pmc-summary FETCH_DIR WRITE_DIR
        python bench.py --pmc-table PMC_DIR [PMC_DIR ...]
@@ -31,31 +47,45 @@ import time
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, TOP/s
 MALL_BYTES = 256 * 2**20
+ROTATION_CAP_BYTES = 48 * 2**30
 METRIC = "quantize GB/s + W4A4 GEMM TOPS on 1 MI355X; % of HBM / i8-MFMA roofline"
 ROOT = os.path.dirname(os.path.abspath(__file__))
+
+# config 5: Llama-3-8B down_proj, bf16 X [T, 14336] -> W [4096, 14336] packed, passed as W.t()
+LIN_K, LIN_N, LIN_M, LIN_NT = 14336, 4096, 112, 128
 
 
 def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _nbuf(bytes_per_set, minimum=2):
-    return max(minimum, math.ceil(1.25 * MALL_BYTES / max(1, bytes_per_set)))
+def _nsets(bytes_per_set, steps):
+    """Buffer sets to rotate: one per step while they fit in ROTATION_CAP_BYTES,
+    never fewer than 1.25 x the MALL's worth."""
+    per = max(1, bytes_per_set)
+    return max(2, math.ceil(1.25 * MALL_BYTES / per), min(steps, ROTATION_CAP_BYTES // per))
 
 
 WARM_S = 0.2   # minimum untimed warm-up per measurement
+MARKER_KERNEL = "FillFunctor<float>"   # ends every measurement in a kernel trace
+_MARKER = []
+
+
+def _marker(torch):
+    """One float32 fill of a single element: a dispatch that separates measurements
+    in a kernel trace (trace_summary starts new segments after it)."""
+    if not _MARKER:
+        _MARKER.append(torch.empty(1, dtype=torch.float32, device="cuda"))
+    _MARKER[0].fill_(0.0)
 
 
 def _time_graph(torch, launch, steps, warmup):
     """Warm up, capture ``steps`` launches in one graph, replay it once timed.
 
     Warm-up: ``warmup`` eager launches, then untimed replays of the same graph
-    for at least WARM_S seconds. Replaying the timed graph itself touches every
-    rotated buffer in the timed order before the timed replay (a shorter
-    warm-up graph left the last buffers' first touch inside the timed
-    replay), and the time floor covers the clock ramp of a GPU that has been
-    idle. Returns (gpu_ms_total, wall_s_total) of the timed replay.
-    ``launch(i)`` issues step i on the current stream.
+    for at least WARM_S seconds (the time floor covers the clock ramp of a GPU
+    that has been idle). Returns (gpu_ms_total, wall_s_total) of the timed
+    replay. ``launch(i)`` issues step i on the current stream.
     """
     for i in range(warmup):
         launch(i)
@@ -83,15 +113,27 @@ def _time_graph(torch, launch, steps, warmup):
     end.record(cur)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    _marker(torch)
     return start.elapsed_time(end), wall
 
+
+def _hbm(gbs):
+    return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
+
+
+def _mfma(tops):
+    return {"bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+            "frac": tops / INT8_PEAK_TOPS}
+
+
+# --------------------------------------------------------------------------- GPU measurements
 
 def bench_quant(torch, case, steps, warmup, dev):
     from quant_ops_amd import capi
 
     t, f = case.x.shape
     per_set = case.algorithmic_bytes()
-    nbuf = _nbuf(per_set)
+    nbuf = _nsets(per_set, steps)
     x0 = case.x.to(dev)
     xs = [x0] + [x0.clone() for _ in range(nbuf - 1)]
     L, R = case.left.to(dev), case.right.to(dev)
@@ -112,9 +154,7 @@ def bench_quant(torch, case, steps, warmup, dev):
         "dtype": str(case.x.dtype).replace("torch.", ""), "clip_ratio": case.clip_ratio,
         "pack_int32": case.pack_int32, "bytes_per_step": per_set, "flops_per_step": case.flops(),
         "buffers_rotated": nbuf, "us_per_step": per_step_s * 1e6, "GBps": gbs,
-        "TFLOPs": case.flops() / per_step_s / 1e12, "wall_s": wall,
-        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": gbs / HBM_PEAK_GBS},
+        "TFLOPs": case.flops() / per_step_s / 1e12, "wall_s": wall, "roofline": _hbm(gbs),
     }
     del xs, codes, scales
     torch.cuda.empty_cache()
@@ -126,7 +166,7 @@ def bench_gemm(torch, case, steps, warmup, dev):
 
     m, n, k = case.mnk
     per_set = case.algorithmic_bytes()
-    nbuf = _nbuf(per_set)
+    nbuf = _nsets(per_set, steps)
     a0, b0 = case.a.to(dev), case.b.to(dev)
     As = [a0] + [a0.clone() for _ in range(nbuf - 1)]
     Bs = [b0] + [b0.clone() for _ in range(nbuf - 1)] if b0.is_contiguous() else \
@@ -145,38 +185,130 @@ def bench_gemm(torch, case, steps, warmup, dev):
         "workload": case.name, "M": m, "N": n, "K": k, "b_layout": "KN" if b0.is_contiguous() else "W.t()",
         "out_dtype": str(case.out_dtype).replace("torch.", ""), "ops_per_step": case.ops(),
         "bytes_per_step": per_set, "buffers_rotated": nbuf, "us_per_step": per_step_s * 1e6, "TOPS": tops,
-        "GBps": per_set / per_step_s / 1e9, "wall_s": wall,
-        "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                     "frac": tops / INT8_PEAK_TOPS},
+        "GBps": per_set / per_step_s / 1e9, "wall_s": wall, "roofline": _mfma(tops),
     }
     del As, Bs, outs
     torch.cuda.empty_cache()
     return out
 
 
-def bench_linear(torch, tokens, steps, warmup, dev):
-    """Config 5: bf16 X [T, 14336] -> quantize (112 x 128, clip 0.9) -> GEMM vs W.t() -> bf16 [T, 4096]."""
-    from quant_ops_amd import capi
+def linear_inputs(torch, tokens):
+    """Config 5's seeded inputs (host tensors): X, L, R, packed W [4096, 1792], its fp16 scales."""
     from quant_ops_amd import workloads as wl
 
-    x = wl.activations(tokens, 14336, torch.bfloat16, seed=21, outlier_frac=0.005, outlier_scale=30.0).to(dev)
-    L, R = wl.orthogonal(112, 22, torch.bfloat16).to(dev), wl.orthogonal(128, 23, torch.bfloat16).to(dev)
-    w = wl.random_packed(4096, 1792, 24).to(dev)
-    sw = wl.uniform(4096, 0.001, 0.01, 25).to(dev)
-    codes = torch.empty(tokens, 1792, dtype=torch.int32, device=dev)
-    scales = torch.empty(tokens, dtype=torch.float32, device=dev)
-    out = torch.empty(tokens, 4096, dtype=torch.bfloat16, device=dev)
+    x = wl.activations(tokens, LIN_K, torch.bfloat16, seed=21, outlier_frac=0.005, outlier_scale=30.0)
+    L, R = wl.orthogonal(LIN_M, 22, torch.bfloat16), wl.orthogonal(LIN_NT, 23, torch.bfloat16)
+    w = wl.random_packed(LIN_N, LIN_K // 8, 24)
+    sw = wl.uniform(LIN_N, 0.001, 0.01, 25)
+    return x, L, R, w, sw
+
+
+def bench_linear(torch, tokens, steps, warmup, dev):
+    """Config 5 at ``tokens``: the step (quantize, then the GEMM against W.t() with
+    bf16 output) and each of its two kernels timed alone, every buffer rotated
+    (X, W, codes, scales, output)."""
+    from quant_ops_amd import capi
+
+    x_h, L_h, R_h, w_h, sw_h = linear_inputs(torch, tokens)
+    L, R, sw = L_h.to(dev), R_h.to(dev), sw_h.to(dev)
+    w_bytes = LIN_N * LIN_K // 2
+    q_bytes = tokens * LIN_K * 2 + tokens * LIN_K // 2 + tokens * 4 + 2 * (LIN_M ** 2 + LIN_NT ** 2)
+    g_bytes = w_bytes + tokens * LIN_K // 2 + tokens * 4 + LIN_N * 2 + tokens * LIN_N * 2
+    per_set = tokens * LIN_K * 2 + w_bytes + tokens * LIN_K // 2 + tokens * 4 + tokens * LIN_N * 2
+    nbuf = _nsets(per_set, steps)
+    x0, w0 = x_h.to(dev), w_h.to(dev)
+    xs = [x0] + [x0.clone() for _ in range(nbuf - 1)]
+    ws = [w0] + [w0.clone() for _ in range(nbuf - 1)]
+    codes = [torch.empty(tokens, LIN_K // 8, dtype=torch.int32, device=dev) for _ in range(nbuf)]
+    scales = [torch.empty(tokens, dtype=torch.float32, device=dev) for _ in range(nbuf)]
+    outs = [torch.empty(tokens, LIN_N, dtype=torch.bfloat16, device=dev) for _ in range(nbuf)]
+
+    def quant(j):
+        capi.flatquant_quantize(xs[j], L, R, 0.9, True, out_codes=codes[j], out_scales=scales[j])
+
+    def gemm(j):
+        capi.int4_gemm(codes[j], ws[j].t(), scales[j], sw, out=outs[j])
+
+    for j in range(nbuf):      # codes of every set, for the GEMM timed alone
+        quant(j)
+    torch.cuda.synchronize()
+    ms_q, _ = _time_graph(torch, lambda i: quant(i % nbuf), steps, warmup)
+    ms_g, _ = _time_graph(torch, lambda i: gemm(i % nbuf), steps, warmup)
+    ms_s, wall = _time_graph(torch, lambda i: (quant(i % nbuf), gemm(i % nbuf)), steps, warmup)
+    t_q, t_g, t_s = (ms / 1e3 / steps for ms in (ms_q, ms_g, ms_s))
+    ops = 2 * tokens * LIN_N * LIN_K
+    gemm_gbs = g_bytes / t_g / 1e9
+    out = {
+        "workload": f"cfg5_w4a4_linear_down_proj_T{tokens}", "tokens": tokens, "K": LIN_K, "N": LIN_N,
+        "buffers_rotated": nbuf, "us_per_step": t_s * 1e6, "quantize_us": t_q * 1e6, "gemm_us": t_g * 1e6,
+        "ops_per_step": ops, "TOPS": ops / t_s / 1e12, "gemm_TOPS": ops / t_g / 1e12,
+        "quantize_bytes": q_bytes, "quantize_GBps": q_bytes / t_q / 1e9,
+        "gemm_bytes": g_bytes, "gemm_GBps": gemm_gbs, "weight_bytes": w_bytes,
+        "weight_GBps_gemm": w_bytes / t_g / 1e9, "weight_GBps_step": w_bytes / t_s / 1e9, "wall_s": wall,
+    }
+    # the dominant kernel: the GEMM; at 16 tokens it is a weight stream (HBM), at 4096 MFMA work
+    out["roofline"] = _hbm(gemm_gbs) if tokens <= 64 else _mfma(ops / t_g / 1e12)
+    del xs, ws, codes, scales, outs
+    torch.cuda.empty_cache()
+    return out
+
+
+def roundtrip_cfg1(torch, dev):
+    """Config 1's round trip through the public API: quantize (int8 codes), then
+    dequantize_int4, on the CPU fallback (use_cuda=False) and on the GPU kernels.
+
+    Errors: ||Yhat - Y|| / ||Y|| with Y = the fallback's transformed X
+    (flatquant/ops.py:99-103) and Yhat the dequantized codes, and
+    ||L Yhat R^T - X|| / ||X|| (X recovered through the inverse of the
+    orthogonal transforms; equal to the first up to rounding).
+    """
+    import quant_ops_amd as qo
+    from quant_ops_amd import workloads as wl
+
+    case = wl.quant_cfg1()
+    t, f = case.x.shape
+    m, n = case.left.shape[0], case.right.shape[0]
+    x, L, R = case.x, case.left, case.right
+    y = torch.matmul(L.T, torch.matmul(x.reshape(-1, m, n), R)).reshape(t, f)
+
+    def errs(yhat):
+        yhat = yhat.float().cpu()
+        xhat = torch.matmul(L, torch.matmul(yhat.reshape(-1, m, n), R.T)).reshape(t, f)
+        return {"rel_err_Y": float((yhat - y).norm() / y.norm()),
+                "rel_err_X": float((xhat - x).norm() / x.norm())}
+
+    q_c, s_c = qo.flatquant_dynamic_quantize(x, L, R, case.clip_ratio, False, use_cuda=False)
+    cpu = errs(qo.dequantize_int4(q_c, s_c, False))
+    q_g, s_g = qo.flatquant_dynamic_quantize(x.to(dev), L.to(dev), R.to(dev), case.clip_ratio, False)
+    gpu = errs(qo.dequantize_int4(q_g, s_g, False))
+    torch.cuda.synchronize()
+    same = bool(torch.equal(q_g.cpu(), q_c) and torch.equal(s_g.cpu(), s_c.float()))
+    return {"cpu_fallback": cpu, "gpu": gpu, "gpu_codes_and_scales_equal_cpu": same,
+            "note": "Y = L^T X R per token (the fallback's transformed X), Yhat = dequantize_int4(codes, scales)"}
+
+
+def bench_copy_probe(torch, steps, warmup, dev, nbytes=20996096):
+    """A plain elementwise copy (torch.neg on fp16) reading and writing half of
+    ``nbytes`` each: config 2's byte count through the simplest streaming kernel,
+    in the same graph timing. Its rate is the floor the config 2 quantize is
+    compared with (launch plus streaming at this size)."""
+    n_el = nbytes // 4
+    per_set = 4 * n_el
+    nbuf = _nsets(per_set, steps)
+    src0 = torch.randn(n_el, dtype=torch.float16, device=dev)
+    srcs = [src0] + [src0.clone() for _ in range(nbuf - 1)]
+    dsts = [torch.empty_like(src0) for _ in range(nbuf)]
 
     def launch(i):
-        capi.flatquant_quantize(x, L, R, 0.9, True, out_codes=codes, out_scales=scales)
-        capi.int4_gemm(codes, w.t(), scales, sw, out=out)
+        torch.neg(srcs[i % nbuf], out=dsts[i % nbuf])
 
-    gpu_ms, wall = _time_graph(torch, launch, steps, warmup)
+    gpu_ms, _ = _time_graph(torch, launch, steps, warmup)
     per_step_s = gpu_ms / 1e3 / steps
-    ops = 2 * tokens * 4096 * 14336
-    return {"workload": f"cfg5_w4a4_linear_down_proj_T{tokens}", "tokens": tokens,
-            "us_per_step": per_step_s * 1e6, "TOPS": ops / per_step_s / 1e12,
-            "weight_GBps": 4096 * 1792 * 4 / per_step_s / 1e9, "note": "quantize + GEMM, L2/MALL-warm inputs"}
+    gbs = per_set / per_step_s / 1e9
+    del srcs, dsts
+    torch.cuda.empty_cache()
+    return {"workload": "torch.neg fp16, 10.5 MB in + 10.5 MB out (config 2's 21.0 MB)", "bytes_per_step": per_set,
+            "buffers_rotated": nbuf, "us_per_step": per_step_s * 1e6, "GBps": gbs, "roofline": _hbm(gbs)}
 
 
 def bench_dequant(torch, steps, warmup, dev):
@@ -190,7 +322,7 @@ def bench_dequant(torch, steps, warmup, dev):
     codes0 = torch.randint(-2**31, 2**31, (t, f // 8), generator=g, dtype=torch.int64).to(torch.int32).to(dev)
     scales0 = torch.rand(t, generator=g).to(dev)
     nbytes = t * f // 2 + t * 4 + t * f * 4
-    nbuf = _nbuf(nbytes)
+    nbuf = _nsets(nbytes, steps)
     codes = [codes0] + [codes0.clone() for _ in range(nbuf - 1)]
     outs = [torch.empty(t, f, dtype=torch.float32, device=dev) for _ in range(nbuf)]
 
@@ -203,9 +335,7 @@ def bench_dequant(torch, steps, warmup, dev):
     del codes, outs
     torch.cuda.empty_cache()
     return {"workload": "dequantize_int4 packed [2048, 512] -> fp32 [2048, 4096]", "bytes_per_step": nbytes,
-            "us_per_step": per_step_s * 1e6, "GBps": gbs, "buffers_rotated": nbuf,
-            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gbs / HBM_PEAK_GBS}}
+            "us_per_step": per_step_s * 1e6, "GBps": gbs, "buffers_rotated": nbuf, "roofline": _hbm(gbs)}
 
 
 LAYOUT_ROWS, LAYOUT_K = 14336, 4096   # the config 4 weight W [N, K] as int8 codes
@@ -231,7 +361,7 @@ def bench_layout(torch, steps, warmup, dev):
     )
     for name, src0, fn, out_shape, out_dtype in cases:
         nbytes = src0.numel() * src0.element_size() + math.prod(out_shape) * torch.empty((), dtype=out_dtype).element_size()
-        nbuf = _nbuf(nbytes)
+        nbuf = _nsets(nbytes, steps)
         srcs = [src0] + [src0.clone() for _ in range(nbuf - 1)]
         dsts = [torch.empty(out_shape, dtype=out_dtype, device=dev) for _ in range(nbuf)]
 
@@ -242,69 +372,106 @@ def bench_layout(torch, steps, warmup, dev):
         per_step_s = gpu_ms / 1e3 / steps
         gbs = nbytes / per_step_s / 1e9
         res[name] = {"bytes_per_step": nbytes, "us_per_step": per_step_s * 1e6, "GBps": gbs, "buffers_rotated": nbuf,
-                     "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                  "frac": gbs / HBM_PEAK_GBS}}
+                     "roofline": _hbm(gbs)}
         del srcs, dsts
     del codes0, words0
     torch.cuda.empty_cache()
     return res
 
 
-def cpu_baseline(torch, budget_s=12.0):
-    """The oracle (CPU restatement of the reference fallback) on config 2, bounded in time."""
-    from oracle import fq_reference as ofq
-    from quant_ops_amd import workloads as wl
+# --------------------------------------------------------------------------- CPU baselines
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    case = wl.quant_cfg2()
-    ofq.flatquant_pytorch(case.x, case.left, case.right, case.clip_ratio, True)   # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        ofq.flatquant_pytorch(case.x, case.left, case.right, case.clip_ratio, True)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    cpu_model = ""
+def _cpu_model():
     try:
         with open("/proc/cpuinfo") as fh:
             for line in fh:
                 if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": case.algorithmic_bytes() / med / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"config 2 in full ([2048, 4096] fp16, packed), median of {len(times)} runs of the "
-                      f"oracle's torch-CPU fallback restatement ({med * 1e3:.1f} ms each); cpu: {cpu_model}; "
-                      f"torch {torch.__version__}"}
+    return "unknown"
 
 
-def cpu_baseline_gemm(torch, budget_s=8.0):
+def _cpu_median(fn, budget_s, min_runs=3):
+    """Median seconds of ``fn()`` after one warm-up call, over at least ``min_runs``
+    runs and ``budget_s`` seconds."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def _cpu_line(torch, value, unit, sample, med, runs):
+    return {"value": value, "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{sample}; median of {runs} runs ({med * 1e3:.1f} ms each) of the oracle's restatement of "
+                      f"the reference's torch-CPU fallback; cpu: {_cpu_model()}; torch {torch.__version__}"}
+
+
+def cpu_quant(torch, case, budget_s, sample):
+    from oracle import fq_reference as ofq
+
+    med, runs = _cpu_median(lambda: ofq.flatquant_pytorch(case.x, case.left, case.right, case.clip_ratio,
+                                                          case.pack_int32), budget_s)
+    return _cpu_line(torch, case.algorithmic_bytes() / med / 1e9, "GB/s", sample, med, runs)
+
+
+def cpu_gemm_cfg4(torch, budget_s):
     """The oracle GEMM (unpack + float32 matmul + scales) on a 128-row slab of config 4."""
     from oracle import int4_reference as oi4
     from quant_ops_amd import workloads as wl
 
     case = wl.gemm_case(128, 14336, 4096, seed=0)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 2:
-        t0 = time.perf_counter()
-        oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b)
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    return {"value": case.ops() / med / 1e12, "unit": "TOP/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"128 x 14336 x 4096 slab of config 4, median of {len(times)} runs ({med:.2f} s each)"}
+    med, runs = _cpu_median(lambda: oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b), budget_s,
+                            min_runs=2)
+    return _cpu_line(torch, case.ops() / med / 1e12, "TOP/s", "128 x 14336 x 4096 slab of config 4 (1/32 of its rows)",
+                     med, runs)
 
+
+def cpu_linear(torch, tokens, sample_tokens, budget_s):
+    """Config 5's step on the CPU (fallback quantize, then the fallback GEMM against
+    W.t()) on ``sample_tokens`` of the ``tokens``-token workload."""
+    from oracle import fq_reference as ofq
+    from oracle import int4_reference as oi4
+
+    x, L, R, w, sw = linear_inputs(torch, sample_tokens)
+
+    def step():
+        q, s = ofq.flatquant_pytorch(x, L, R, 0.9, True)
+        oi4.int4_matmul_pytorch(q, w.t(), s, sw)
+
+    med, runs = _cpu_median(step, budget_s, min_runs=2)
+    ops = 2 * sample_tokens * LIN_N * LIN_K
+    what = "all 16 tokens" if sample_tokens == tokens else f"{sample_tokens} of its {tokens} tokens"
+    return _cpu_line(torch, ops / med / 1e12, "TOP/s", f"config 5 step (quantize + GEMM, bf16 out) on {what}",
+                     med, runs)
+
+
+def cpu_dequant(torch, budget_s):
+    from oracle import fq_reference as ofq
+
+    t, f = 2048, 4096
+    g = torch.Generator().manual_seed(52)
+    codes = torch.randint(-2**31, 2**31, (t, f // 8), generator=g, dtype=torch.int64).to(torch.int32)
+    scales = torch.rand(t, generator=g)
+    med, runs = _cpu_median(lambda: ofq.dequantize_int4(codes, scales, True), budget_s)
+    return _cpu_line(torch, (t * f // 2 + t * 4 + t * f * 4) / med / 1e9, "GB/s",
+                     "config 2's packed codes in full", med, runs)
+
+
+# --------------------------------------------------------------------------- profiling helpers
 
 # Kernel of each benched workload, as rocprofv3 names it (a substring of the demangled name).
 KERNEL_OF = {
+    "gemm_cfg4": "gemm_i4_pp<256, 224, 4, 2, 4, false, qo::OutF16>",
     "quantize_cfg2": "fq_wave_kernel<qo::F16T, 4, 2, true>",
     "quantize_cfg3": "fq_duo_kernel<qo::BF16T, 7, true>",
-    "gemm_cfg4": "gemm_i4_pp<256, 224, 4, 2, 4, false, qo::OutF16>",
+    "gemm_cfg5_T16": "gemm_i4_skinny_nk",
+    "gemm_cfg5_T4096": "gemm_i4_pp<256, 256, 4, 2, 4, true, qo::OutBF16>",
 }
 COPY_PROBE_BYTES = 1 << 30      # float32 negation of 1 GiB: reads and writes exactly this many bytes
 COPY_PROBE_KERNEL = "neg_kernel"
@@ -320,6 +487,14 @@ def pmc_pass(torch, dev):
     from quant_ops_amd import capi
     from quant_ops_amd import workloads as wl
 
+    case = wl.gemm_cfg4()
+    a, b = case.a.to(dev), case.b.to(dev)
+    sa, sb = case.scale_a.to(dev), case.scale_b.to(dev)
+    for _ in range(4):
+        out = torch.empty(case.mnk[:2], dtype=case.out_dtype, device=dev)
+        capi.int4_gemm(a.clone(), b.clone(), sa, sb, out=out)
+        torch.cuda.synchronize()
+    del a, b, out
     for case in (wl.quant_cfg2(), wl.quant_cfg3()):
         t, f = case.x.shape
         x = case.x.to(dev)
@@ -331,14 +506,18 @@ def pmc_pass(torch, dev):
             capi.flatquant_quantize(xi, L, R, case.clip_ratio, True, out_codes=codes, out_scales=scales)
             torch.cuda.synchronize()
         del x, xi, codes, scales
-    case = wl.gemm_cfg4()
-    a, b = case.a.to(dev), case.b.to(dev)
-    sa, sb = case.scale_a.to(dev), case.scale_b.to(dev)
-    for _ in range(4):
-        out = torch.empty(case.mnk[:2], dtype=case.out_dtype, device=dev)
-        capi.int4_gemm(a.clone(), b.clone(), sa, sb, out=out)
-        torch.cuda.synchronize()
-    del a, b, out
+    for tokens in (16, 4096):
+        x_h, L_h, R_h, w_h, sw_h = linear_inputs(torch, tokens)
+        L, R, sw = L_h.to(dev), R_h.to(dev), sw_h.to(dev)
+        codes = torch.empty(tokens, LIN_K // 8, dtype=torch.int32, device=dev)
+        scales = torch.empty(tokens, dtype=torch.float32, device=dev)
+        capi.flatquant_quantize(x_h.to(dev), L, R, 0.9, True, out_codes=codes, out_scales=scales)
+        w = w_h.to(dev)
+        for _ in range(4):
+            out = torch.empty(tokens, LIN_N, dtype=torch.bfloat16, device=dev)
+            capi.int4_gemm(codes.clone(), w.clone().t(), scales, sw, out=out)
+            torch.cuda.synchronize()
+        del w, out, codes, scales
     src = torch.randn(COPY_PROBE_BYTES // 4, device=dev)
     dst = torch.empty_like(src)
     for _ in range(4):
@@ -367,12 +546,12 @@ def pmc_table(dirs):
                     vals[key] = vals.get(key, 0.0) + float(row["Counter_Value"])
     counters = sorted({c for c, _, _ in vals})
     names = list(KERNEL_OF)
-    print(f"{'counter':34s} " + " ".join(f"{n:>14s}" for n in names))
+    print(f"{'counter':34s} " + " ".join(f"{n:>16s}" for n in names))
     for c in counters:
         cells = []
         for n in names:
             hits = [v for (cc, kn, _), v in vals.items() if cc == c and KERNEL_OF[n] in kn]
-            cells.append(f"{statistics.median(hits):14.4g}" if hits else f"{'-':>14s}")
+            cells.append(f"{statistics.median(hits):16.4g}" if hits else f"{'-':>16s}")
         print(f"{c:34s} " + " ".join(cells))
 
 
@@ -425,14 +604,21 @@ def pmc_summary(fetch_dir, write_dir):
     print(json.dumps(out, indent=1))
 
 
+def _lin_q_bytes(t):
+    return t * LIN_K * 2 + t * LIN_K // 2 + t * 4 + 2 * (LIN_M ** 2 + LIN_NT ** 2)
+
+
 # Workloads in the order the default bench run dispatches them (one segment of
-# launches each; the config 5 linear interleaves its two kernels).
+# launches each, in order of first dispatch; a config 5 step interleaves its
+# two kernels, which then form one segment each).
 BENCH_SEGMENTS = [
-    ("quantize cfg2", 20996096, None), ("gemm cfg4", None, 481036337152), ("quantize cfg3", 293691904, None),
-    ("cfg5 T=16 quantize", 16 * 14336 * 2 + 16 * 1792 * 4 + 16 * 4 + 2 * (112 * 112 + 128 * 128), None),
-    ("cfg5 T=16 gemm", None, 2 * 16 * 4096 * 14336),
-    ("cfg5 T=4096 quantize", 4096 * 14336 * 2 + 4096 * 1792 * 4 + 4096 * 4 + 2 * (112 * 112 + 128 * 128), None),
-    ("cfg5 T=4096 gemm", None, 2 * 4096 * 4096 * 14336),
+    ("gemm cfg4", None, 481036337152), ("quantize cfg2", 20996096, None),
+    ("copy probe cfg2 bytes", 20996096, None), ("quantize cfg3", 293691904, None),
+    ("cfg5 T=16 quantize", _lin_q_bytes(16), None), ("cfg5 T=16 gemm", None, 2 * 16 * LIN_N * LIN_K),
+    ("cfg5 T=16 step quant", _lin_q_bytes(16), None), ("cfg5 T=16 step gemm", None, 2 * 16 * LIN_N * LIN_K),
+    ("cfg5 T=4096 quantize", _lin_q_bytes(4096), None), ("cfg5 T=4096 gemm", None, 2 * 4096 * LIN_N * LIN_K),
+    ("cfg5 T=4096 step quant", _lin_q_bytes(4096), None), ("cfg5 T=4096 step gemm", None, 2 * 4096 * LIN_N * LIN_K),
+    ("quantize cfg1", 128 * 4096 * 4 + 128 * 4096 + 128 * 4 + 2 * 64 * 64 * 4, None),
     ("pack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
     ("unpack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
     ("transpose cfg4 weight", 2 * 14336 * 512 * 4, None),
@@ -443,31 +629,36 @@ BENCH_SEGMENTS = [
 def trace_summary(trace_csv, tail=None):
     """Per-workload kernel durations from a rocprofv3 --kernel-trace CSV of a default bench run.
 
-    Dispatches of this library's kernels are split into segments (a new segment
-    starts when a kernel reappears after more than 16 other dispatches) and the
-    segments, in dispatch order, are matched to BENCH_SEGMENTS. With ``tail``,
-    only the last ``tail`` dispatches of each segment count (the timed steps;
-    the warm-up replays come first).
+    Every measurement ends with one marker dispatch (MARKER_KERNEL). Between two
+    markers, the dispatches of each of this library's kernels (and of the copy
+    probe) form one segment; segments in order of first dispatch are matched to
+    BENCH_SEGMENTS. With ``tail``, only the last ``tail`` dispatches of each
+    segment count (the timed steps; the warm-up comes first) and segments with
+    fewer dispatches (single eager calls outside the measurements) are left out.
     """
     import csv
     import statistics
 
-    rows = [r for r in csv.DictReader(open(trace_csv)) if "qo::" in r["Kernel_Name"]]
-    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
-    segs, last = [], {}
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Dispatch_Id"]))
+    segs, cur, epoch = [], {}, 0
     for r in rows:
-        key = (r["Kernel_Name"], r["Grid_Size_X"], r["Workgroup_Size_X"])
-        did = int(r["Dispatch_Id"])
-        if key not in last or did - last[key][0] > 16:
-            seg = {"key": key, "first": did, "dur": []}
-            segs.append(seg)
-            last[key] = (did, seg)
-        seg = last[key][1]
-        last[key] = (did, seg)
-        seg["dur"].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        name = r["Kernel_Name"]
+        if MARKER_KERNEL in name:
+            epoch += 1
+            cur = {}
+            continue
+        if "qo::" not in name and COPY_PROBE_KERNEL not in name:
+            continue
+        key = (name, r["Grid_Size_X"], r["Workgroup_Size_X"])
+        if key not in cur:
+            cur[key] = {"key": key, "first": int(r["Dispatch_Id"]), "dur": []}
+            segs.append(cur[key])
+        cur[key]["dur"].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    if tail:
+        segs = [s for s in segs if len(s["dur"]) >= tail]
     segs.sort(key=lambda s: s["first"])
     labelled = len(segs) == len(BENCH_SEGMENTS)
-    lines = [f"{'workload':22s} {'calls':>5s} {'avg_us':>9s} {'median_us':>9s} {'min_us':>9s} {'max_us':>9s} "
+    lines = [f"{'workload':24s} {'calls':>5s} {'avg_us':>9s} {'median_us':>9s} {'min_us':>9s} {'max_us':>9s} "
              f"{'GB/s':>7s} {'TOP/s':>7s}  kernel [grid x block]"]
     for i, s in enumerate(segs):
         d = s["dur"][-tail:] if tail else s["dur"]
@@ -475,8 +666,8 @@ def trace_summary(trace_csv, tail=None):
         name, nbytes, ops = BENCH_SEGMENTS[i] if labelled else (f"segment {i}", None, None)
         gbs = f"{nbytes / avg / 1e3:7.0f}" if nbytes else f"{'':7s}"
         tops = f"{ops / avg / 1e6:7.0f}" if ops else f"{'':7s}"
-        kname = s["key"][0].split("(")[0].replace("void ", "")
-        lines.append(f"{name:22s} {len(d):5d} {avg:9.2f} {statistics.median(d) / 1e3:9.2f} {min(d) / 1e3:9.2f} "
+        kname = s["key"][0].split("(")[0].replace("void ", "")[:110]
+        lines.append(f"{name:24s} {len(d):5d} {avg:9.2f} {statistics.median(d) / 1e3:9.2f} {min(d) / 1e3:9.2f} "
                      f"{max(d) / 1e3:9.2f} {gbs} {tops}  {kname} [{s['key'][1]} x {s['key'][2]}]")
     print("\n".join(lines))
 
@@ -493,16 +684,18 @@ def _traffic_from_profiles(kernel_key):
         return None
 
 
+# --------------------------------------------------------------------------- main
+
 def main():
     global WARM_S
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--warm-s", type=float, default=WARM_S,
                     help="minimum seconds of untimed warm-up replays per measurement (default %(default)s)")
-    ap.add_argument("--no-secondary", action="store_true", help="only the primary workload")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-secondary", action="store_true", help="only the headline workload")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="eager launches of each benched kernel and a copy probe, for rocprofv3 --pmc")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
@@ -548,62 +741,76 @@ def main():
     if args.pmc_pass:
         pmc_pass(torch, dev)
         return
+    steps, warmup = args.steps, args.warmup
 
-    _log("primary: config 2 quantize")
-    primary = bench_quant(torch, wl.quant_cfg2(), args.steps, args.warmup, dev)
-    primary["roofline"]["traffic"] = _traffic_from_profiles("quantize_cfg2")
-    _log(f"config 2: {primary['us_per_step']:.2f} us/step, {primary['GBps']:.0f} GB/s")
-
-    secondary = {}
+    _log("headline: config 4 GEMM")
+    head = bench_gemm(torch, wl.gemm_cfg4(), steps, warmup, dev)
+    head["roofline"]["traffic"] = _traffic_from_profiles("gemm_cfg4")
+    _log(f"config 4: {head['us_per_step']:.1f} us/step, {head['TOPS']:.0f} TOP/s")
+    lines = {"gemm_cfg4": head}
     if not args.no_secondary:
-        _log("secondary: config 4 GEMM")
-        secondary["gemm_cfg4"] = bench_gemm(torch, wl.gemm_cfg4(), args.steps, args.warmup, dev)
-        secondary["gemm_cfg4"]["roofline"]["traffic"] = _traffic_from_profiles("gemm_cfg4")
-        _log(f"config 4: {secondary['gemm_cfg4']['us_per_step']:.1f} us/step, "
-             f"{secondary['gemm_cfg4']['TOPS']:.0f} TOPS")
-        _log("secondary: config 3 quantize")
-        secondary["quantize_cfg3"] = bench_quant(torch, wl.quant_cfg3(), args.steps, args.warmup, dev)
-        secondary["quantize_cfg3"]["roofline"]["traffic"] = _traffic_from_profiles("quantize_cfg3")
-        _log(f"config 3: {secondary['quantize_cfg3']['us_per_step']:.1f} us/step, "
-             f"{secondary['quantize_cfg3']['GBps']:.0f} GB/s")
+        _log("config 2 quantize")
+        lines["quantize_cfg2"] = bench_quant(torch, wl.quant_cfg2(), steps, warmup, dev)
+        lines["quantize_cfg2"]["roofline"]["traffic"] = _traffic_from_profiles("quantize_cfg2")
+        lines["copy_probe_cfg2_bytes"] = bench_copy_probe(torch, steps, warmup, dev)
+        _log(f"config 2: {lines['quantize_cfg2']['us_per_step']:.2f} us/step "
+             f"(copy of the same bytes {lines['copy_probe_cfg2_bytes']['us_per_step']:.2f} us)")
+        _log("config 3 quantize")
+        lines["quantize_cfg3"] = bench_quant(torch, wl.quant_cfg3(), steps, warmup, dev)
+        lines["quantize_cfg3"]["roofline"]["traffic"] = _traffic_from_profiles("quantize_cfg3")
+        _log(f"config 3: {lines['quantize_cfg3']['us_per_step']:.1f} us/step")
         for t in (16, 4096):
-            _log(f"secondary: config 5 linear T={t}")
-            secondary[f"linear_cfg5_T{t}"] = bench_linear(torch, t, args.steps, args.warmup, dev)
-        _log("secondary: weight layout kernels (config 4 weight)")
-        secondary["layout_cfg4_weight"] = bench_layout(torch, args.steps, args.warmup, dev)
-        _log("secondary: dequantize (config 2 codes)")
-        secondary["dequant_cfg2"] = bench_dequant(torch, args.steps, args.warmup, dev)
+            _log(f"config 5 linear T={t}")
+            key = f"linear_cfg5_T{t}"
+            lines[key] = bench_linear(torch, t, steps, warmup, dev)
+            lines[key]["roofline"]["traffic"] = _traffic_from_profiles(f"gemm_cfg5_T{t}")
+            _log(f"config 5 T={t}: {lines[key]['us_per_step']:.1f} us/step (quantize {lines[key]['quantize_us']:.1f}, "
+                 f"GEMM {lines[key]['gemm_us']:.1f})")
+        _log("config 1 round trip + quantize")
+        rt = roundtrip_cfg1(torch, dev)
+        lines["quantize_cfg1"] = bench_quant(torch, wl.quant_cfg1(), steps, warmup, dev)
+        lines["quantize_cfg1"]["round_trip"] = rt
+        _log("weight layout kernels (config 4 weight)")
+        lines["layout_cfg4_weight"] = bench_layout(torch, steps, warmup, dev)
+        _log("dequantize (config 2 codes)")
+        lines["dequant_cfg2"] = bench_dequant(torch, steps, warmup, dev)
 
-    cpu = None
     if not args.no_cpu:
-        _log("cpu baseline (oracle on host cores)")
-        cpu = cpu_baseline(torch)
+        _log("cpu baselines (oracle on host cores)")
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        head["cpu_baseline"] = cpu_gemm_cfg4(torch, 6.0)
         if not args.no_secondary:
-            secondary["gemm_cfg4"]["cpu_baseline"] = cpu_baseline_gemm(torch)
+            lines["quantize_cfg2"]["cpu_baseline"] = cpu_quant(torch, wl.quant_cfg2(), 5.0, "config 2 in full")
+            lines["quantize_cfg3"]["cpu_baseline"] = cpu_quant(torch, wl.quant_cfg3(tokens=1024), 4.0,
+                                                               "1024 of config 3's 8192 tokens")
+            lines["linear_cfg5_T16"]["cpu_baseline"] = cpu_linear(torch, 16, 16, 4.0)
+            lines["linear_cfg5_T4096"]["cpu_baseline"] = cpu_linear(torch, 4096, 128, 4.0)
+            lines["quantize_cfg1"]["cpu_baseline"] = cpu_quant(torch, wl.quant_cfg1(), 2.0, "config 1 in full")
+            lines["dequant_cfg2"]["cpu_baseline"] = cpu_dequant(torch, 2.0)
 
     line = {
         "metric": METRIC,
-        "value": primary["GBps"],
-        "unit": "GB/s",
+        "value": head["TOPS"],
+        "unit": "TOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": primary["us_per_step"] / 1e3,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": head["us_per_step"] / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic: seeded N(0,1) activations with 1% of channels x20, orthogonal transforms from QR "
-                "of seeded Gaussians",
+        "dtype": "i8",
+        "data": "synthetic: seeded uniform int4 codes in [-8, 7] packed 8 per int32, fp16 scales U(0.01, 0.1) per "
+                "token and U(0.001, 0.01) per channel; quantize lines: seeded N(0,1) activations with outlier "
+                "channels, orthogonal transforms from QR of seeded Gaussians",
         "config": {
-            "workload": "BASELINE config 2: flatquant_dynamic_quantize fp16 X[2048,4096], M=N=64, "
-                        "clip_ratio=0.9, pack_int32=True (one step = one quantize call)",
-            "tokens": 2048, "features": 4096, "M": 64, "N": 64,
+            "workload": "BASELINE config 4: int4_matmul A [4096, 4096/8] x B [4096/8, 14336] int32-packed int4, "
+                        "int32 accumulate on the i8 MFMA, fp16 out (one step = one GEMM call)",
+            "M": 4096, "N": 14336, "K": 4096,
         },
-        "roofline": primary["roofline"],
-        "cpu_baseline": cpu,
-        "primary": primary,
-        "secondary": secondary,
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "lines": lines,
     }
     print(json.dumps(line), flush=True)
 

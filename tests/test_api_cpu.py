@@ -3,6 +3,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -293,3 +294,16 @@ def test_pybind_equivalents_check_arguments_like_the_reference():
     b = torch.zeros(1, 3, dtype=torch.int32)
     with pytest.raises(RuntimeError, match="a_packed must be on CUDA"):
         extension.cuda_int4_matmul(a, b, torch.ones(2), torch.ones(3))
+
+
+def test_bench_rotation_and_gpu_count(tmp_path):
+    """bench.py gives every timed step its own buffer set while the sets fit,
+    never fewer than 1.25 x the MALL's worth, and refuses more than one GPU."""
+    import bench
+
+    assert bench._nsets(155_226_112, 20) == 20                # config 4: one set per step
+    assert bench._nsets(20_996_096, 5) == 16                 # few steps: still past the MALL
+    assert bench._nsets(300_000_000, 1000) == bench.ROTATION_CAP_BYTES // 300_000_000
+    proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                          capture_output=True, text=True)
+    assert proc.returncode == 2 and "one GPU only" in proc.stderr
