@@ -38,7 +38,7 @@ enum qo_status {
   QO_ERR_DTYPE = 3,         /* dtype code not supported for that operand */
   QO_ERR_ALIGNMENT = 4,     /* pointer / stride not aligned as required */
   QO_ERR_UNSUPPORTED = 5,   /* valid request this build does not implement */
-  QO_ERR_LAUNCH = 6         /* hipLaunchKernel (or hipGetLastError) failed */
+  QO_ERR_LAUNCH = 6         /* hipLaunchKernel of this call failed */
 };
 
 /* Human-readable name of a status code (static storage). */
@@ -49,6 +49,27 @@ const char* qo_version(void);
 
 /* Message of the last failed call on this host thread ("" if none). */
 const char* qo_last_error(void);
+
+/*
+ * Kernel routing overrides, process-wide. Each QO_ROUTE_* bit takes one kernel
+ * family out of the dispatch so that the fallback kernel for the same shape
+ * runs instead; results are the same to the parity bars. Returns the previous
+ * mask. Meant for cross-checking kernels against each other (the test suite)
+ * and for diagnosis; production callers leave it at 0. No counterpart in the
+ * reference (its dispatch has one kernel per operator). Calls racing with
+ * quantize / GEMM calls on other threads see either mask.
+ */
+enum qo_route {
+  QO_ROUTE_FQ_GENERIC = 1u << 0,     /* quantize: every shape on the generic kernel */
+  QO_ROUTE_FQ_NO_WAVE = 1u << 1,     /* quantize: no one-wave-per-token kernel */
+  QO_ROUTE_FQ_NO_DUO = 1u << 2,      /* quantize: no two-waves-per-token kernel */
+  QO_ROUTE_FQ_NO_FEW = 1u << 3,      /* quantize: no few-token routing to the workgroup kernel */
+  QO_ROUTE_GEMM_GENERIC = 1u << 4,   /* GEMM: every shape on the generic kernel */
+  QO_ROUTE_GEMM_NO_DMA = 1u << 5,    /* GEMM: no LDS-DMA tiled kernel */
+  QO_ROUTE_GEMM_NO_SKINNY = 1u << 6, /* GEMM: no small-M kernels */
+  QO_ROUTE_ALL = (1u << 7) - 1u
+};
+unsigned qo_set_kernel_routing(unsigned mask);
 
 /*
  * Fused FlatQuant dynamic int4 quantization, one pass over X.
@@ -70,8 +91,14 @@ const char* qo_last_error(void);
  *                  8p..8p+7, code i in bits 4i..4i+3 as (q + 8)
  *   out_scales  float32 [tokens]: the scale rounded to x_dtype, as float32
  *
+ * Any M and N up to M = 2559 are accepted; shapes outside the MFMA kernels'
+ * tables run a VALU kernel with the same rounding points (slower), and those
+ * whose X and Z rows exceed the LDS (fp32 above 20480 features, fp16 / bf16
+ * above 40960) compute Y by column blocks.
+ *
  * Errors: QO_ERR_SHAPE if M*N % 8 != 0 while pack_int32, tokens < 0, M or N < 1;
- * QO_ERR_DTYPE for other x_dtype codes.
+ * QO_ERR_DTYPE for other x_dtype codes; QO_ERR_UNSUPPORTED for M > 2559 on
+ * the column-block path.
  */
 int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
                           const void* left, const void* right, int M, int N,

@@ -6,6 +6,7 @@ kernels through it; torch tensors are only used here to own device memory and
 to name the current stream. Every call raises ``QuantOpsError`` on a non-zero
 status, with the library's message.
 """
+import contextlib
 import ctypes
 import os
 
@@ -18,9 +19,13 @@ STATUS = {0: "QO_OK", 1: "QO_ERR_NULL_POINTER", 2: "QO_ERR_SHAPE", 3: "QO_ERR_DT
           4: "QO_ERR_ALIGNMENT", 5: "QO_ERR_UNSUPPORTED", 6: "QO_ERR_LAUNCH"}
 
 # Every symbol the header declares; the CPU tests check they are all exported.
-EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_flatquant_quantize",
+EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_set_kernel_routing", "qo_flatquant_quantize",
             "qo_int4_gemm", "qo_int4_gemm_bias", "qo_dequantize_int4", "qo_pack_int4_to_int32", "qo_unpack_int32_to_int4",
             "qo_transpose_int32")
+
+# QO_ROUTE_* bits of qo_set_kernel_routing (include/quant_ops_hip.h)
+ROUTE = {"FQ_GENERIC": 1 << 0, "FQ_NO_WAVE": 1 << 1, "FQ_NO_DUO": 1 << 2, "FQ_NO_FEW": 1 << 3,
+         "GEMM_GENERIC": 1 << 4, "GEMM_NO_DMA": 1 << 5, "GEMM_NO_SKINNY": 1 << 6}
 
 _TORCH_CODE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
@@ -49,6 +54,8 @@ def lib():
     L.qo_version.argtypes = []
     L.qo_last_error.restype = ctypes.c_char_p
     L.qo_last_error.argtypes = []
+    L.qo_set_kernel_routing.restype = ctypes.c_uint
+    L.qo_set_kernel_routing.argtypes = [ctypes.c_uint]
     L.qo_flatquant_quantize.restype = c_int
     L.qo_flatquant_quantize.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_int,
                                         c_vp, c_vp, c_vp]
@@ -83,6 +90,29 @@ def _stream(stream):
 
 def version() -> str:
     return lib().qo_version().decode()
+
+
+def set_kernel_routing(mask: int) -> int:
+    """Set the process-wide QO_ROUTE_* mask; returns the previous one."""
+    return int(lib().qo_set_kernel_routing(mask))
+
+
+def route_mask(*names) -> int:
+    mask = 0
+    for name in names:
+        mask |= ROUTE[name]
+    return mask
+
+
+@contextlib.contextmanager
+def kernel_routing(*names):
+    """Add the named QO_ROUTE_* bits (``ROUTE`` keys) for the duration of the block."""
+    prev = set_kernel_routing(0)
+    set_kernel_routing(prev | route_mask(*names))
+    try:
+        yield
+    finally:
+        set_kernel_routing(prev)
 
 
 def flatquant_quantize(x, left, right, clip_ratio=1.0, pack_int32=False, out_codes=None, out_scales=None,

@@ -6,6 +6,11 @@
 
 static thread_local char g_last_error[512] = "";
 
+namespace qo {
+std::atomic<unsigned> g_route_mask{0u};
+thread_local hipError_t g_launch_error = hipSuccess;
+}  // namespace qo
+
 void qo_set_error(const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -16,6 +21,10 @@ void qo_set_error(const char* fmt, ...) {
 extern "C" const char* qo_last_error(void) { return g_last_error; }
 
 extern "C" const char* qo_version(void) { return "0.1.0"; }
+
+extern "C" unsigned qo_set_kernel_routing(unsigned mask) {
+  return qo::g_route_mask.exchange(mask & QO_ROUTE_ALL, std::memory_order_relaxed);
+}
 
 extern "C" const char* qo_status_string(int status) {
   switch (status) {

@@ -5,6 +5,9 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <tuple>
+#include <type_traits>
+#include <utility>
 
 #include "quant_ops_hip.h"
 
@@ -171,3 +174,49 @@ __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 
 // Thread-local error message used by qo_last_error().
 void qo_set_error(const char* fmt, ...);
+
+namespace qo {
+
+// Kernel routing overrides set through qo_set_kernel_routing (QO_ROUTE_* bits):
+// one relaxed atomic load per dispatch decision.
+extern std::atomic<unsigned> g_route_mask;
+inline bool route_off(unsigned bit) { return (g_route_mask.load(std::memory_order_relaxed) & bit) != 0u; }
+
+// Kernel launches of one C-ABI call. launch() starts a kernel with
+// hipLaunchKernel (arguments converted to the kernel's parameter types) and
+// keeps the first failure of the current call; launch_result() reports it.
+// Errors that earlier, unrelated work left on the thread are neither reported
+// as this call's nor consumed; an error of a launch made here is taken off the
+// thread (hipGetLastError) so that the caller's next check does not see it
+// again.
+extern thread_local hipError_t g_launch_error;
+
+inline void launch_begin() { g_launch_error = hipSuccess; }
+
+template <class K, class Tup, size_t... I>
+inline hipError_t launch_tuple(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Tup& args,
+                               std::index_sequence<I...>) {
+  void* ptrs[] = {static_cast<void*>(&std::get<I>(args))...};
+  return hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, lds, stream);
+}
+
+template <class... P, class... A>
+inline void launch(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t stream, A&&... args) {
+  static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+  std::tuple<std::decay_t<P>...> vals(std::forward<A>(args)...);
+  const hipError_t e = launch_tuple(kernel, grid, block, lds, stream, vals, std::index_sequence_for<P...>{});
+  if (e != hipSuccess) {
+    if (g_launch_error == hipSuccess) g_launch_error = e;
+    (void)hipGetLastError();
+  }
+}
+
+inline int launch_result(const char* who) {
+  const hipError_t e = g_launch_error;
+  g_launch_error = hipSuccess;
+  if (e == hipSuccess) return QO_OK;
+  qo_set_error("%s: launch failed: %s", who, hipGetErrorString(e));
+  return QO_ERR_LAUNCH;
+}
+
+}  // namespace qo

@@ -96,6 +96,7 @@ extern "C" int qo_dequantize_int4(const void* codes, int pack_int32, const void*
     return QO_ERR_NULL_POINTER;
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  launch_begin();
   const bool vec = (features % 8 == 0) && ((uintptr_t)out % 16 == 0) && (pack_int32 || (uintptr_t)codes % 8 == 0);
   if (vec) {
     const int64_t wpr = features / 8;
@@ -104,26 +105,21 @@ extern "C" int qo_dequantize_int4(const void* codes, int pack_int32, const void*
     if (pack_int32) {
       const int64_t bx = (wpr + 255) / 256;
       const unsigned by = (unsigned)std::min<int64_t>(tokens, 65535);
-      hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)bx, by), dim3(256), 0, s,
+      launch(dequant_rows_kernel, dim3((unsigned)bx, by), dim3(256), 0, s,
                          reinterpret_cast<const int32_t*>(codes), scales, scale_dtype, tokens, wpr, out);
     }
     else
-      hipLaunchKernelGGL(dequant_i8_kernel, dim3((unsigned)blocks), dim3(256), 0, s, codes, scales, scale_dtype,
+      launch(dequant_i8_kernel, dim3((unsigned)blocks), dim3(256), 0, s, codes, scales, scale_dtype,
                          tokens, wpr, out);
   } else {
     int64_t blocks = (tokens * features + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (pack_int32)
-      hipLaunchKernelGGL(dequant_packed_any, dim3((unsigned)blocks), dim3(256), 0, s,
+      launch(dequant_packed_any, dim3((unsigned)blocks), dim3(256), 0, s,
                          reinterpret_cast<const int32_t*>(codes), scales, scale_dtype, tokens, features, out);
     else
-      hipLaunchKernelGGL(dequant_i8_any, dim3((unsigned)blocks), dim3(256), 0, s,
+      launch(dequant_i8_any, dim3((unsigned)blocks), dim3(256), 0, s,
                          reinterpret_cast<const int8_t*>(codes), scales, scale_dtype, tokens, features, out);
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    qo_set_error("qo_dequantize_int4: launch failed: %s", hipGetErrorString(e));
-    return QO_ERR_LAUNCH;
-  }
-  return QO_OK;
+  return launch_result("qo_dequantize_int4");
 }

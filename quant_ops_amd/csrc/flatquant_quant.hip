@@ -17,7 +17,11 @@
 //                       or LDS, R in VGPRs.
 //  * fq_generic_kernel — any M, N, D in {fp32, fp16, bf16}; VALU fp32 FMA with the
 //                       same rounding points. Used for shapes the MFMA kernels
-//                       do not cover (and for fp32 inputs).
+//                       do not cover (and for fp32 inputs), X and Z in LDS.
+//  * fq_generic_big_kernel — the same results where X and Z do not fit in LDS
+//                       (fp32 above 20480 features, other shapes above 40960):
+//                       Y by blocks of 16 columns, computed twice per token.
+//                       M up to 2559.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -179,6 +183,88 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
       }
     }
     __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernel for shapes whose X and Z do not fit in LDS together (fp32
+// above 20480 features, fp16 / bf16 shapes outside the MFMA kernels above
+// 40960): one 256-thread block per token (grid-stride over tokens). Y is
+// computed in blocks of kBigCols columns: Z's block [M, kBigCols] in LDS, X,
+// L and R read through the caches. It runs twice per token, once for the
+// extremes (the scale) and once more, with the same arithmetic and so the
+// same values, for the codes. Rounding points and the sequential float32 sums
+// over k are those of fq_generic_kernel, so the results are identical.
+// ---------------------------------------------------------------------------
+constexpr int kBigCols = 16;
+
+template <class DT, bool PACK>
+__global__ void __launch_bounds__(256)
+fq_generic_big_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+                      const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, int M,
+                      int N, float clip, void* __restrict__ out_codes, float* __restrict__ out_scales) {
+  extern __shared__ __align__(16) float zb[];   // [M][kBigCols], D values as float
+  __shared__ float red_hi[4], red_lo[4], s_scale;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t F = (int64_t)M * N;
+  for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
+    const typename DT::T* xt = x + t * x_ld;
+    float hi = -INFINITY, lo = INFINITY, s = 0.f;
+    for (int pass = 0; pass < 2; ++pass) {
+      if (pass == 1 && PACK) {
+        // nibbles are ORed in below, a block of columns at a time
+        int32_t* o = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8);
+        for (int64_t p = tid; p < F / 8; p += 256) o[p] = 0;
+        __syncthreads();
+      }
+      for (int n0 = 0; n0 < N; n0 += kBigCols) {
+        const int cb = min(kBigCols, N - n0);
+        // Z[:, n0 .. n0 + cb) = rnd_D(X R[:, n0 .. n0 + cb))
+        for (int o = tid; o < M * cb; o += 256) {
+          const int m = o / cb, j = o % cb;
+          float acc = 0.f;
+          for (int k = 0; k < N; ++k) acc = fmaf(DT::to_f(xt[(int64_t)m * N + k]), DT::to_f(right[k * N + n0 + j]), acc);
+          zb[m * kBigCols + j] = DT::round(acc);
+        }
+        __syncthreads();
+        // Y[:, n0 .. n0 + cb) = rnd_D(L^T Z[:, n0 .. n0 + cb))
+        for (int o = tid; o < M * cb; o += 256) {
+          const int m = o / cb, j = o % cb;
+          float acc = 0.f;
+          for (int k = 0; k < M; ++k) acc = fmaf(DT::to_f(left[k * M + m]), zb[k * kBigCols + j], acc);
+          const float y = DT::round(acc);
+          if (pass == 0) {
+            hi = fmaxf(hi, y);
+            lo = fminf(lo, y);
+          } else {
+            const int64_t f = (int64_t)m * N + n0 + j;
+            const float q = DT::round(opaque(y) / s);
+            if (PACK) {
+              const uint32_t nib = (uint32_t)(fq_code_from_quot<true>(q) + 8) << (4 * (f & 7));
+              atomicOr(reinterpret_cast<uint32_t*>(out_codes) + t * (F / 8) + (f >> 3), nib);
+            } else {
+              reinterpret_cast<int8_t*>(out_codes)[t * F + f] = (int8_t)fq_code_from_quot<false>(q);
+            }
+          }
+        }
+        __syncthreads();
+      }
+      if (pass == 0) {
+        hi = wave_max(hi);
+        lo = wave_min(lo);
+        if (lane == 0) { red_hi[wave] = hi; red_lo[wave] = lo; }
+        __syncthreads();
+        if (tid == 0) {
+          float h = red_hi[0], l = red_lo[0];
+          for (int w = 1; w < 4; ++w) { h = fmaxf(h, red_hi[w]); l = fminf(l, red_lo[w]); }
+          const float sc = fq_scale<DT>(h, l, clip);
+          s_scale = sc;
+          out_scales[t] = sc;
+        }
+        __syncthreads();
+        s = s_scale;
+      }
+    }
   }
 }
 
@@ -676,7 +762,9 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform, so in SGPRs: the LDS-DMA destinations (M0 values) derived
+  // from it then need no VGPRs across the token loop
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tau = wave / NP;   // token slot of this wave
   const int q = wave % NP;     // column pair of this wave
   const int li = lane & 15;    // lane row / column inside a 16x16 block
@@ -1509,7 +1597,7 @@ static int launch_mfma(const void* x, int64_t tokens, int64_t x_ld, const void* 
   const int64_t ngroups = (tokens + S::TPB - 1) / S::TPB;
   int64_t grid = (int64_t)device_cu_count() * per_cu;
   if (grid > ngroups) grid = ngroups;
-  hipLaunchKernelGGL((fq_mfma_kernel<DT, MB, NP, PACK, NV, MV>), dim3((unsigned)grid), dim3(S::WAVES * 64), 0, stream,
+  launch((fq_mfma_kernel<DT, MB, NP, PACK, NV, MV>), dim3((unsigned)grid), dim3(S::WAVES * 64), 0, stream,
                      reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
                      reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
   return QO_OK;
@@ -1522,7 +1610,7 @@ static int launch_wave(const void* x, int64_t tokens, int64_t x_ld, const void* 
   // one token per wave, up to two workgroups per CU; beyond that waves loop
   const int64_t grid = std::min<int64_t>((tokens + kWaveKernelWaves - 1) / kWaveKernelWaves,
                                          (int64_t)device_cu_count() * 2);
-  hipLaunchKernelGGL((fq_wave_kernel<DT, MB, NQ, PACK>), dim3((unsigned)grid), dim3(64 * kWaveKernelWaves), 0,
+  launch((fq_wave_kernel<DT, MB, NQ, PACK>), dim3((unsigned)grid), dim3(64 * kWaveKernelWaves), 0,
                      stream,
                      reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
                      reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
@@ -1536,32 +1624,29 @@ static int launch_duo(const void* x, int64_t tokens, int64_t x_ld, const void* l
   constexpr int SLOTS = DuoShape<MB>::SLOTS;
   // one workgroup (four waves, one per SIMD) per CU
   const int64_t grid = std::min<int64_t>((tokens + SLOTS - 1) / SLOTS, (int64_t)device_cu_count());
-  hipLaunchKernelGGL((fq_duo_kernel<DT, MB, PACK>), dim3((unsigned)grid), dim3(128 * SLOTS), 0, stream,
+  launch((fq_duo_kernel<DT, MB, PACK>), dim3((unsigned)grid), dim3(128 * SLOTS), 0, stream,
                      reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
                      reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
   return QO_OK;
 }
 
-// QO_FQ_NO_DUO=1 keeps N = 128 shapes on fq_mfma_kernel (tests use it to
+// QO_ROUTE_FQ_NO_DUO keeps N = 128 shapes on fq_mfma_kernel (tests use it to
 // cross-check the two).
 static bool fq_allow_duo() {
-  const char* e = getenv("QO_FQ_NO_DUO");
-  return !(e && e[0] == '1');
+  return !route_off(QO_ROUTE_FQ_NO_DUO);
 }
 
-// QO_FQ_NO_WAVE=1 keeps small shapes on fq_mfma_kernel (tests use it to
+// QO_ROUTE_FQ_NO_WAVE keeps small shapes on fq_mfma_kernel (tests use it to
 // cross-check the two MFMA kernels).
 static bool fq_allow_wave() {
-  const char* e = getenv("QO_FQ_NO_WAVE");
-  return !(e && e[0] == '1');
+  return !route_off(QO_ROUTE_FQ_NO_WAVE);
 }
 
-// QO_FQ_NO_FEW=1 keeps the one-wave and pair kernels at any token count
+// QO_ROUTE_FQ_NO_FEW keeps the one-wave and pair kernels at any token count
 // (tests use it to cross-check them against the workgroup kernel on small
 // inputs).
 static bool fq_route_few() {
-  const char* e = getenv("QO_FQ_NO_FEW");
-  return !(e && e[0] == '1');
+  return !route_off(QO_ROUTE_FQ_NO_FEW);
 }
 
 template <class DT, bool PACK>
@@ -1660,6 +1745,23 @@ static int launch_generic(const void* x, int64_t tokens, int64_t x_ld, const voi
                           int M, int N, float clip, void* out_codes, float* out_scales, hipStream_t stream) {
   using T = typename DT::T;
   const size_t lds = (size_t)2 * M * N * sizeof(T);
+  constexpr size_t kMaxDynLds = 160 * 1024 - 64;   // the static reduction slots take the rest
+  if (lds > kMaxDynLds) {
+    // X and Z do not fit together: Y by column blocks, twice per token
+    const size_t zb = (size_t)M * kBigCols * sizeof(float);
+    auto big = fq_generic_big_kernel<DT, PACK>;
+    if (zb > kMaxDynLds ||
+        (zb > 64 * 1024 &&
+         hipFuncSetAttribute((const void*)big, hipFuncAttributeMaxDynamicSharedMemorySize, (int)zb) != hipSuccess)) {
+      qo_set_error("qo_flatquant_quantize: M=%d needs %zu bytes of LDS for a Z column block", M, zb);
+      return QO_ERR_UNSUPPORTED;
+    }
+    int64_t grid = (int64_t)device_cu_count() * 4;
+    if (grid > tokens) grid = tokens;
+    launch(big, dim3((unsigned)grid), dim3(256), zb, stream, reinterpret_cast<const T*>(x), tokens, x_ld,
+           reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), M, N, clip, out_codes, out_scales);
+    return QO_OK;
+  }
   auto kern = fq_generic_kernel<DT, PACK>;
   if (lds > 64 * 1024) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
@@ -1670,7 +1772,7 @@ static int launch_generic(const void* x, int64_t tokens, int64_t x_ld, const voi
   }
   int64_t grid = (int64_t)device_cu_count() * 4;
   if (grid > tokens) grid = tokens;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), lds, stream, reinterpret_cast<const T*>(x), tokens,
+  launch(kern, dim3((unsigned)grid), dim3(256), lds, stream, reinterpret_cast<const T*>(x), tokens,
                      x_ld, reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), M, N, clip,
                      out_codes, out_scales);
   return QO_OK;
@@ -1697,11 +1799,10 @@ static int run_quantize(const void* x, int64_t tokens, int64_t x_ld, const void*
 
 }  // namespace qo
 
-// Selects the kernel family; QO_FQ_FORCE_GENERIC=1 in the environment routes
-// every shape through the generic kernel (tests use it to cross-check the two).
+// Selects the kernel family; QO_ROUTE_FQ_GENERIC routes every shape through
+// the generic kernel (tests use it to cross-check the two).
 static bool fq_allow_mfma() {
-  const char* e = getenv("QO_FQ_FORCE_GENERIC");
-  return !(e && e[0] == '1');
+  return !qo::route_off(QO_ROUTE_FQ_GENERIC);
 }
 
 extern "C" int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
@@ -1728,6 +1829,7 @@ extern "C" int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens,
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool mf = fq_allow_mfma();
+  launch_begin();
   int st;
   switch (x_dtype) {
     case QO_DTYPE_F32:
@@ -1752,11 +1854,6 @@ extern "C" int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens,
       qo_set_error("qo_flatquant_quantize: unsupported input dtype code %d", x_dtype);
       return QO_ERR_DTYPE;
   }
-  if (st != QO_OK) return st;
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    qo_set_error("qo_flatquant_quantize: launch failed: %s", hipGetErrorString(e));
-    return QO_ERR_LAUNCH;
-  }
-  return QO_OK;
+  const int lst = launch_result("qo_flatquant_quantize");
+  return st != QO_OK ? st : lst;
 }

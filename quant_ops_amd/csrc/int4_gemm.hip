@@ -1024,11 +1024,10 @@ gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __r
 // Host dispatch.
 // ---------------------------------------------------------------------------
 
-// QO_GEMM_NO_DMA=1 keeps the register-staged MFMA kernel for every shape
+// QO_ROUTE_GEMM_NO_DMA keeps the register-staged MFMA kernel for every shape
 // (tests use it to cross-check the two MFMA kernels).
 static bool gemm_allow_dma() {
-  const char* e = getenv("QO_GEMM_NO_DMA");
-  return !(e && e[0] == '1');
+  return !route_off(QO_ROUTE_GEMM_NO_DMA);
 }
 
 template <class OT>
@@ -1036,7 +1035,7 @@ static void launch_generic(const int32_t* a, int64_t lda, const int32_t* b, int6
                            const void* sa, int sad, const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int64_t M,
                            int64_t N, int64_t K, hipStream_t stream) {
   dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
-  hipLaunchKernelGGL(gemm_i4_generic<OT>, grid, dim3(256), 0, stream, a, lda, b, bsp, bsn, sa, sad, sb, sbd,
+  launch(gemm_i4_generic<OT>, grid, dim3(256), 0, stream, a, lda, b, bsp, bsn, sa, sad, sb, sbd,
                      reinterpret_cast<typename OT::T*>(out), ldc, reinterpret_cast<const typename OT::T*>(bias), M, N, K / 8);
 }
 
@@ -1044,7 +1043,7 @@ template <int BM, int BN, int BK, int WGM, int WGN, bool B_NK, class OT>
 static void launch_mfma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
                         const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K, hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_i4_mfma<BM, BN, BK, WGM, WGN, B_NK, OT>), dim3(tiles_m * tiles_n),
+  launch((gemm_i4_mfma<BM, BN, BK, WGM, WGN, B_NK, OT>), dim3(tiles_m * tiles_n),
                      dim3(64 * WGM * WGN), 0, stream, a, lda,
                      b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, reinterpret_cast<const typename OT::T*>(bias), M, N, K, tiles_m,
                      tiles_n);
@@ -1055,7 +1054,7 @@ template <int BM, int BN, bool B_NK, class OT>
 static void launch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
                        const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K, hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_i4_pp<BM, BN, 4, 2, 4, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a, lda,
+  launch((gemm_i4_pp<BM, BN, 4, 2, 4, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a, lda,
                      b, ldb, sa, sad, sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc,
                      reinterpret_cast<const typename OT::T*>(bias), M, N, K, tiles_m);
 }
@@ -1081,11 +1080,10 @@ static void dispatch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_
     launch_dma<256, 256, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
 }
 
-// QO_GEMM_NO_SKINNY=1 sends small M to the tiled kernels (tests use it to
+// QO_ROUTE_GEMM_NO_SKINNY sends small M to the tiled kernels (tests use it to
 // cross-check the two).
 static bool gemm_allow_skinny() {
-  const char* e = getenv("QO_GEMM_NO_SKINNY");
-  return !(e && e[0] == '1');
+  return !route_off(QO_ROUTE_GEMM_NO_SKINNY);
 }
 
 template <class OT>
@@ -1096,10 +1094,10 @@ static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64
   using T = typename OT::T;
   auto go = [&](auto mt, auto nk_layout) {
     if constexpr (decltype(nk_layout)::value)
-      hipLaunchKernelGGL((gemm_i4_skinny_nk<decltype(mt)::value, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb,
+      launch((gemm_i4_skinny_nk<decltype(mt)::value, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb,
                          sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
     else
-      hipLaunchKernelGGL((gemm_i4_skinny<decltype(mt)::value, false, OT>), grid, dim3(512), 0, stream, a, lda, b,
+      launch((gemm_i4_skinny<decltype(mt)::value, false, OT>), grid, dim3(512), 0, stream, a, lda, b,
                          ldb, sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N,
                          K);
   };
@@ -1153,11 +1151,10 @@ static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bs
 
 }  // namespace qo
 
-// QO_GEMM_FORCE_GENERIC=1 routes every call through the generic kernel (tests
+// QO_ROUTE_GEMM_GENERIC routes every call through the generic kernel (tests
 // use it to cross-check the two).
 static bool gemm_allow_fast() {
-  const char* e = getenv("QO_GEMM_FORCE_GENERIC");
-  return !(e && e[0] == '1');
+  return !qo::route_off(QO_ROUTE_GEMM_GENERIC);
 }
 
 static bool is_float_code(int d) { return d == QO_DTYPE_F32 || d == QO_DTYPE_F16 || d == QO_DTYPE_BF16; }
@@ -1192,6 +1189,7 @@ static int gemm_entry(const char* who, const int32_t* a, int64_t lda, const int3
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool fast = gemm_allow_fast();
+  launch_begin();
   switch (out_dtype) {
     case QO_DTYPE_F16:
       dispatch<OutF16>(a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b, scale_b_dtype, out, ldc,
@@ -1206,12 +1204,7 @@ static int gemm_entry(const char* who, const int32_t* a, int64_t lda, const int3
                        bias, M, N, K, s, fast);
       break;
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    qo_set_error("%s: launch failed: %s", who, hipGetErrorString(e));
-    return QO_ERR_LAUNCH;
-  }
-  return QO_OK;
+  return launch_result(who);
 }
 
 extern "C" int qo_int4_gemm(const int32_t* a, int64_t lda, const int32_t* b, int64_t b_stride_p,

@@ -157,14 +157,6 @@ static unsigned grid_for(int64_t items) {
   return (unsigned)(blocks < 1 ? 1 : blocks);
 }
 
-static int launch_status(const char* who) {
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    qo_set_error("%s: launch failed: %s", who, hipGetErrorString(e));
-    return QO_ERR_LAUNCH;
-  }
-  return QO_OK;
-}
 
 }  // namespace qo
 
@@ -183,18 +175,19 @@ extern "C" int qo_pack_int4_to_int32(const int8_t* codes, int64_t codes_ld, int6
     return QO_ERR_NULL_POINTER;
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  launch_begin();
   const bool vec = features % 16 == 0 && (uintptr_t)codes % 16 == 0 && (uintptr_t)out % 8 == 0 &&
                    (rows == 1 || (codes_ld % 16 == 0 && out_ld % 2 == 0));
   if (vec) {
     const int64_t pairs = features / 16;
-    hipLaunchKernelGGL(pack_kernel_v16, dim3(grid_for(rows * pairs)), dim3(256), 0, s, codes, codes_ld, rows, pairs,
+    launch(pack_kernel_v16, dim3(grid_for(rows * pairs)), dim3(256), 0, s, codes, codes_ld, rows, pairs,
                        out, out_ld);
   } else {
     const int64_t wpr = features / 8;
-    hipLaunchKernelGGL(pack_kernel_any, dim3(grid_for(rows * wpr)), dim3(256), 0, s, codes, codes_ld, rows, wpr, out,
+    launch(pack_kernel_any, dim3(grid_for(rows * wpr)), dim3(256), 0, s, codes, codes_ld, rows, wpr, out,
                        out_ld);
   }
-  return launch_status("qo_pack_int4_to_int32");
+  return launch_result("qo_pack_int4_to_int32");
 }
 
 extern "C" int qo_unpack_int32_to_int4(const int32_t* words, int64_t words_ld, int64_t rows, int64_t nwords,
@@ -211,17 +204,18 @@ extern "C" int qo_unpack_int32_to_int4(const int32_t* words, int64_t words_ld, i
     return QO_ERR_NULL_POINTER;
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  launch_begin();
   const bool vec = nwords % 2 == 0 && (uintptr_t)words % 8 == 0 && (uintptr_t)out % 16 == 0 &&
                    (rows == 1 || (words_ld % 2 == 0 && out_ld % 16 == 0));
   if (vec) {
     const int64_t pairs = nwords / 2;
-    hipLaunchKernelGGL(unpack_kernel_v16, dim3(grid_for(rows * pairs)), dim3(256), 0, s, words, words_ld, rows,
+    launch(unpack_kernel_v16, dim3(grid_for(rows * pairs)), dim3(256), 0, s, words, words_ld, rows,
                        pairs, out, out_ld);
   } else {
-    hipLaunchKernelGGL(unpack_kernel_any, dim3(grid_for(rows * nwords)), dim3(256), 0, s, words, words_ld, rows,
+    launch(unpack_kernel_any, dim3(grid_for(rows * nwords)), dim3(256), 0, s, words, words_ld, rows,
                        nwords, out, out_ld);
   }
-  return launch_status("qo_unpack_int32_to_int4");
+  return launch_result("qo_unpack_int32_to_int4");
 }
 
 extern "C" int qo_transpose_int32(const int32_t* in, int64_t in_ld, int64_t rows, int64_t cols, int32_t* out,
@@ -247,11 +241,12 @@ extern "C" int qo_transpose_int32(const int32_t* in, int64_t in_ld, int64_t rows
   // (and everything otherwise) move one word per access
   const bool vec = (uintptr_t)in % 16 == 0 && (uintptr_t)out % 16 == 0 && (rows == 1 || in_ld % 4 == 0) &&
                    (cols == 1 || out_ld % 4 == 0);
+  launch_begin();
   if (vec)
-    hipLaunchKernelGGL(transpose_words_kernel<true>, dim3((unsigned)(tiles_r * tiles_c)), dim3(256), 0,
+    launch(transpose_words_kernel<true>, dim3((unsigned)(tiles_r * tiles_c)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), in, in_ld, rows, cols, out, out_ld, tiles_c);
   else
-    hipLaunchKernelGGL(transpose_words_kernel<false>, dim3((unsigned)(tiles_r * tiles_c)), dim3(256), 0,
+    launch(transpose_words_kernel<false>, dim3((unsigned)(tiles_r * tiles_c)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), in, in_ld, rows, cols, out, out_ld, tiles_c);
-  return launch_status("qo_transpose_int32");
+  return launch_result("qo_transpose_int32");
 }

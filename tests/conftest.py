@@ -22,3 +22,21 @@ def gpu():
 
     assert quant_ops_amd.CUDA_AVAILABLE, f"HIP library not loaded: {quant_ops_amd._loader.LOAD_ERROR}"
     return torch.device("cuda", 0)
+
+
+@pytest.fixture
+def routing():
+    """Switch kernel families off for one test (QO_ROUTE_* bits through the C
+    ABI's qo_set_kernel_routing); the mask is cleared at teardown."""
+    from quant_ops_amd import capi
+
+    class Routing:
+        def on(self, *names):
+            capi.set_kernel_routing(capi.set_kernel_routing(0) | capi.route_mask(*names))
+
+        def off(self, *names):
+            capi.set_kernel_routing(capi.set_kernel_routing(0) & ~capi.route_mask(*names))
+
+    capi.set_kernel_routing(0)
+    yield Routing()
+    capi.set_kernel_routing(0)

@@ -307,3 +307,16 @@ def test_bench_rotation_and_gpu_count(tmp_path):
     proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                           capture_output=True, text=True)
     assert proc.returncode == 2 and "one GPU only" in proc.stderr
+
+
+def test_kernel_routing_mask_round_trips():
+    """qo_set_kernel_routing keeps only the QO_ROUTE_* bits and returns the previous mask."""
+    prev = capi.set_kernel_routing(capi.route_mask("FQ_GENERIC", "GEMM_NO_DMA"))
+    try:
+        assert capi.set_kernel_routing(0xFFFFFFFF) == capi.route_mask("FQ_GENERIC", "GEMM_NO_DMA")
+        assert capi.set_kernel_routing(0) == sum(capi.ROUTE.values())
+        with capi.kernel_routing("FQ_NO_DUO"):
+            assert capi.set_kernel_routing(capi.route_mask("FQ_NO_DUO")) == capi.route_mask("FQ_NO_DUO")
+        assert capi.set_kernel_routing(0) == 0
+    finally:
+        capi.set_kernel_routing(prev)

@@ -205,14 +205,14 @@ def test_quantize_shapes(gpu, t, m, n, dtype, clip, pack):
                                 (108, 128), (32, 48), (64, 88), (80, 112), (40, 64), (72, 96), (76, 128),
                                 (128, 148), (128, 172), (144, 192), (160, 160),
                                 (64, 214), (128, 256), (168, 176)])
-def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
+def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, routing):
     m, n = mn
     case = wl.quant_case("xcheck", 37, m, n, dtype, 0.9, True, seed=5, outlier_frac=0.005, outlier_scale=30.0)
     _say(f"mfma vs generic {m}x{n} {dtype}")
     q1, s1 = run_capi_quant(case, gpu)
-    monkeypatch.setenv("QO_FQ_FORCE_GENERIC", "1")
+    routing.on("FQ_GENERIC")
     q2, s2 = run_capi_quant(case, gpu)
-    monkeypatch.delenv("QO_FQ_FORCE_GENERIC")
+    routing.off("FQ_GENERIC")
     d = (_codes_int8(q1, True).int() - _codes_int8(q2, True).int()).abs()
     assert int(d.max()) <= 1 and float((d != 0).float().mean()) <= CODE_FLIP_FRAC
     assert float(((s1 - s2).abs() / s2.abs()).max()) <= SCALE_RTOL
@@ -222,7 +222,7 @@ def test_quantize_mfma_matches_generic_kernel(gpu, dtype, mn, monkeypatch):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mn", [(64, 64), (32, 64), (32, 32)])
 @pytest.mark.parametrize("tokens", [1, 203, 4099])
-def test_quantize_wave_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack, monkeypatch):
+def test_quantize_wave_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack, routing):
     """The wave-per-token kernel and the workgroup kernel use the same fragment
     layouts and k order, so their codes and scales agree bit for bit."""
     m, n = mn
@@ -230,11 +230,11 @@ def test_quantize_wave_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack,
                          outlier_scale=20.0)
     case.x[tokens // 2].zero_()
     _say(f"wave vs group kernel T={tokens} {m}x{n} {dtype} pack={pack}")
-    monkeypatch.setenv("QO_FQ_NO_FEW", "1")        # the wave kernel also below its token threshold
+    routing.on("FQ_NO_FEW")        # the wave kernel also below its token threshold
     q1, s1 = run_capi_quant(case, gpu)
-    monkeypatch.setenv("QO_FQ_NO_WAVE", "1")
+    routing.on("FQ_NO_WAVE")
     q2, s2 = run_capi_quant(case, gpu)
-    monkeypatch.delenv("QO_FQ_NO_WAVE")
+    routing.off("FQ_NO_WAVE")
     assert torch.equal(s1, s2) and torch.equal(q1, q2)
 
 
@@ -242,7 +242,7 @@ def test_quantize_wave_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack,
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mn", [(112, 128), (64, 128), (128, 128), (96, 128)])
 @pytest.mark.parametrize("tokens", [1, 37, 1030])
-def test_quantize_pair_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack, monkeypatch):
+def test_quantize_pair_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack, routing):
     """The two-waves-per-token kernel (N = 128) and the workgroup kernel use the
     same fragment layouts and k order, so their codes and scales agree bit for
     bit; 1030 tokens make each workgroup loop over several tokens."""
@@ -251,26 +251,26 @@ def test_quantize_pair_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack,
                          outlier_scale=30.0)
     case.x[tokens // 2].zero_()
     _say(f"pair vs group kernel T={tokens} {m}x{n} {dtype} pack={pack}")
-    monkeypatch.setenv("QO_FQ_NO_FEW", "1")        # the pair kernel also below its token threshold
+    routing.on("FQ_NO_FEW")        # the pair kernel also below its token threshold
     q1, s1 = run_capi_quant(case, gpu)
-    monkeypatch.setenv("QO_FQ_NO_DUO", "1")
+    routing.on("FQ_NO_DUO")
     q2, s2 = run_capi_quant(case, gpu)
-    monkeypatch.delenv("QO_FQ_NO_DUO")
+    routing.off("FQ_NO_DUO")
     assert torch.equal(s1, s2) and torch.equal(q1, q2)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mn", [(64, 64), (112, 128), (16, 16)])
-def test_quantize_matches_sequential_accumulation_oracle(gpu, dtype, mn, monkeypatch):
+def test_quantize_matches_sequential_accumulation_oracle(gpu, dtype, mn, routing):
     """Against the fallback with its GEMM summation order fixed (sequential float32):
     the generic kernel is bit-exact, the MFMA kernel differs only where its
     internal summation order rounds Z or Y differently."""
     m, n = mn
     case = wl.quant_case("seq", 512, m, n, dtype, 0.9, True, seed=17, outlier_frac=0.01, outlier_scale=20.0)
     q_ref, s_ref = ofq.flatquant_sequential(case.x, case.left, case.right, 0.9, True)
-    monkeypatch.setenv("QO_FQ_FORCE_GENERIC", "1")
+    routing.on("FQ_GENERIC")
     qg, sg = run_capi_quant(case, gpu)
-    monkeypatch.delenv("QO_FQ_FORCE_GENERIC")
+    routing.off("FQ_GENERIC")
     _say(f"sequential oracle {m}x{n} {dtype}")
     assert torch.equal(sg.cpu(), s_ref.float()) and torch.equal(qg.cpu(), q_ref)
     qm, sm = run_capi_quant(case, gpu)
@@ -282,8 +282,31 @@ def test_quantize_matches_sequential_accumulation_oracle(gpu, dtype, mn, monkeyp
     assert float(srel) <= SCALE_RTOL and same >= 0.99
 
 
+@pytest.mark.parametrize("t,m,n,dtype,pack", [
+    (3, 128, 256, torch.float32, True),     # fp32, 32768 features: X and Z exceed the LDS
+    (2, 128, 256, torch.float32, False),
+    (3, 208, 256, torch.float16, True),     # 53248 (a 405B down_proj width), outside the MFMA tables
+    (2, 208, 256, torch.bfloat16, False),
+    (2, 160, 164, torch.float32, True),     # N % 8 != 0: packed words straddle rows
+])
+def test_quantize_column_block_kernel(gpu, t, m, n, dtype, pack):
+    """Shapes whose X and Z rows do not fit in LDS run the column-block generic
+    kernel: within the north-star bars of the fallback and, for fp16 / bf16
+    (whose products are exact in float32, so the kernel's fused multiply-adds
+    round as the oracle's separate steps do), bit-exact against the fallback
+    with sequential float32 sums (the generic kernels' order)."""
+    case = wl.quant_case(f"big_{m}x{n}_{str(dtype)[6:]}", t, m, n, dtype, 0.9, pack, seed=m + n,
+                         outlier_frac=0.01, outlier_scale=20.0)
+    _say(f"column-block kernel {case.name} pack={pack}")
+    q, s = run_capi_quant(case, gpu)
+    if dtype != torch.float32:
+        q_seq, s_seq = ofq.flatquant_sequential(case.x, case.left, case.right, 0.9, pack)
+        assert torch.equal(s.cpu(), s_seq.float()) and torch.equal(q.cpu(), q_seq)
+    check_quant(case.x, case.left, case.right, 0.9, pack, q, s, case.name)
+
+
 @pytest.mark.parametrize("pack", [True, False])
-def test_quantize_misaligned_outputs(gpu, pack, monkeypatch):
+def test_quantize_misaligned_outputs(gpu, pack, routing):
     """Code output not 16-byte aligned (a view 4 bytes / 3 bytes into a buffer):
     the vector-storing kernels are skipped for the generic one, whose results
     equal the generic kernel's on aligned outputs; nothing outside the view is
@@ -299,9 +322,9 @@ def test_quantize_misaligned_outputs(gpu, pack, monkeypatch):
         codes = big[3:3 + t * f].view(t, f)
     _say(f"quantize misaligned codes pack={pack}")
     q, s = capi.flatquant_quantize(x, L, R, 0.9, pack, out_codes=codes)
-    monkeypatch.setenv("QO_FQ_FORCE_GENERIC", "1")
+    routing.on("FQ_GENERIC")
     q_ref, s_ref = capi.flatquant_quantize(x, L, R, 0.9, pack)
-    monkeypatch.delenv("QO_FQ_FORCE_GENERIC")
+    routing.off("FQ_GENERIC")
     torch.cuda.synchronize()
     assert torch.equal(q, q_ref) and torch.equal(s, s_ref)
     lo = 1 if pack else 3
@@ -356,6 +379,31 @@ def test_quantize_torch_op_matches_capi_and_stream(gpu):
     # use_cuda=False keeps the reference fallback semantics (scale in the input dtype)
     q4, s4 = qo.flatquant_dynamic_quantize(case.x, case.left, case.right, 0.9, True, use_cuda=False)
     assert s4.dtype == torch.float16
+
+
+def test_stale_hip_error_is_neither_reported_nor_consumed(gpu):
+    """An error that earlier work left on the thread (here: hipSetDevice of a
+    device that does not exist) is not reported as the launch failure of the
+    next call, and is still there for its owner to read."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipSetDevice.argtypes = [ctypes.c_int]
+    hip.hipSetDevice.restype = ctypes.c_int
+    hip.hipGetLastError.restype = ctypes.c_int
+    case = wl.quant_cfg2(tokens=64, seed=12)
+    x, L, R = case.x.to(gpu), case.left.to(gpu), case.right.to(gpu)
+    codes = torch.empty(64, 512, dtype=torch.int32, device=gpu)
+    scales = torch.empty(64, dtype=torch.float32, device=gpu)
+    q_ref, s_ref = capi.flatquant_quantize(x, L, R, 0.9, True)
+    torch.cuda.synchronize()
+    assert hip.hipGetLastError() == 0
+    assert hip.hipSetDevice(1 << 20) != 0          # leaves an invalid-device error on the thread
+    capi.flatquant_quantize(x, L, R, 0.9, True, out_codes=codes, out_scales=scales)
+    assert hip.hipGetLastError() != 0              # still the caller's to read
+    assert hip.hipGetLastError() == 0
+    torch.cuda.synchronize()
+    assert torch.equal(codes, q_ref) and torch.equal(scales, s_ref)
 
 
 def test_pybind_equivalents_match_the_operators(gpu):
@@ -475,16 +523,16 @@ def test_gemm_small_bit_exact(gpu, m, n, k, bview):
 @pytest.mark.parametrize("m,n,k", [(1, 4, 128), (16, 16, 128), (300, 260, 1024), (257, 516, 2048),
                                    (512, 448, 512), (256, 224, 384), (33, 12, 256), (1024, 1792, 1152)])
 @pytest.mark.parametrize("bview", [False, True])
-def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, monkeypatch):
+def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, routing):
     case = wl.gemm_case(m, n, k, seed=3 * m + n + k, b_transposed_view=bview)
     _say(f"gemm dma {m}x{n}x{k} bview={bview}")
     a, b = case.a.to(gpu), case.b.to(gpu)
     one_a, one_b = torch.ones(m, device=gpu), torch.ones(n, device=gpu)
     acc = capi.int4_gemm(a, b, one_a, one_b, out_dtype=torch.float32)
     out = capi.int4_gemm(a, b, case.scale_a.to(gpu), case.scale_b.to(gpu))
-    monkeypatch.setenv("QO_GEMM_NO_DMA", "1")
+    routing.on("GEMM_NO_DMA")
     out_old = capi.int4_gemm(a, b, case.scale_a.to(gpu), case.scale_b.to(gpu))
-    monkeypatch.delenv("QO_GEMM_NO_DMA")
+    routing.off("GEMM_NO_DMA")
     torch.cuda.synchronize()
     assert torch.equal(acc.cpu().to(torch.int64), _gemm_ref_acc(case.a, case.b).to(torch.int64))
     assert torch.equal(out.cpu(), oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b))
@@ -497,16 +545,16 @@ def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, monkeypatch):
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 14336), (16, 4096, 14336), (7, 100, 128), (32, 36, 640),
                                    (48, 520, 1152), (64, 64, 4096), (5, 8, 896)])
 @pytest.mark.parametrize("bview", [False, True])
-def test_gemm_skinny_bit_exact(gpu, m, n, k, bview, monkeypatch):
+def test_gemm_skinny_bit_exact(gpu, m, n, k, bview, routing):
     case = wl.gemm_case(m, n, k, seed=5 * m + n + k, b_transposed_view=bview)
     _say(f"gemm skinny {m}x{n}x{k} bview={bview}")
     a, b = case.a.to(gpu), case.b.to(gpu)
     sa, sb = case.scale_a.to(gpu), case.scale_b.to(gpu)
     out = capi.int4_gemm(a, b, sa, sb, out_dtype=torch.bfloat16)
     acc = capi.int4_gemm(a, b, torch.ones(m, device=gpu), torch.ones(n, device=gpu), out_dtype=torch.float32)
-    monkeypatch.setenv("QO_GEMM_NO_SKINNY", "1")
+    routing.on("GEMM_NO_SKINNY")
     out_tiled = capi.int4_gemm(a, b, sa, sb, out_dtype=torch.bfloat16)
-    monkeypatch.delenv("QO_GEMM_NO_SKINNY")
+    routing.off("GEMM_NO_SKINNY")
     torch.cuda.synchronize()
     assert torch.equal(acc.cpu().to(torch.int64), _gemm_ref_acc(case.a, case.b).to(torch.int64))
     assert torch.equal(out.cpu(), oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b,
@@ -580,7 +628,7 @@ def test_gemm_scale_and_out_dtypes(gpu, sdt, odt):
 @pytest.mark.parametrize("path,m,n,k,bview", [
     ("skinny", 16, 300, 1024, True), ("tiled", 300, 260, 2048, False), ("tiled", 257, 516, 1024, True),
     ("mfma", 96, 160, 544, False), ("generic", 33, 70, 136, True)])
-def test_gemm_bias_fused_bit_exact(gpu, odt, path, m, n, k, bview, monkeypatch):
+def test_gemm_bias_fused_bit_exact(gpu, odt, path, m, n, k, bview, routing):
     """The bias epilogue of every GEMM path equals the reference's separate
     `output + bias.to(dtype)` after int4_matmul: two roundings to the output
     dtype (w4a4_flatquant_dynamic.py:262-264)."""
@@ -588,7 +636,7 @@ def test_gemm_bias_fused_bit_exact(gpu, odt, path, m, n, k, bview, monkeypatch):
     g = torch.Generator().manual_seed(m + k)
     bias = (torch.randn(n, generator=g) * 4).to(torch.bfloat16)   # converted to odt as the reference does
     if path == "generic":
-        monkeypatch.setenv("QO_GEMM_FORCE_GENERIC", "1")
+        routing.on("GEMM_GENERIC")
     _say(f"gemm bias {path} {m}x{n}x{k} bview={bview} {odt}")
     out = capi.int4_gemm(case.a.to(gpu), case.b.to(gpu), case.scale_a.to(gpu), case.scale_b.to(gpu),
                          out_dtype=odt, bias=bias.to(gpu))
@@ -600,13 +648,13 @@ def test_gemm_bias_fused_bit_exact(gpu, odt, path, m, n, k, bview, monkeypatch):
     assert torch.equal(op.cpu(), ref)
 
 
-def test_gemm_fast_matches_generic(gpu, monkeypatch):
+def test_gemm_fast_matches_generic(gpu, routing):
     case = wl.gemm_case(512, 384, 2048, seed=12, b_transposed_view=True)
     args = (case.a.to(gpu), case.b.to(gpu), case.scale_a.to(gpu), case.scale_b.to(gpu))
     o1 = capi.int4_gemm(*args)
-    monkeypatch.setenv("QO_GEMM_FORCE_GENERIC", "1")
+    routing.on("GEMM_GENERIC")
     o2 = capi.int4_gemm(*args)
-    monkeypatch.delenv("QO_GEMM_FORCE_GENERIC")
+    routing.off("GEMM_GENERIC")
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
 
