@@ -9,6 +9,7 @@
 // Kernels:
 //  * fq_wave_kernel   — one wave per token, M, N <= 64 (fp16 / bf16).
 //  * fq_duo_kernel    — a pair of waves per token, N = 128, M in {64, 96, 112, 128}.
+//  * fq_few_kernel    — the same shapes at up to 128 tokens: four waves per token.
 //  * fq_mfma_kernel   — D in {fp16, bf16}, the listed shapes: M up to 176 zero-padded
 //                       to 16 MB, N even up to 256 zero-padded to 32 NP.
 //                       Both contractions on v_mfma_f32_16x16x32_{f16,bf16}; X is
@@ -578,7 +579,8 @@ __device__ inline void fq_store_int8_split(int8_t* o, uint32_t lo4, uint32_t hi4
 // One token group (this wave's token slot and pair) from an X stage in LDS:
 // both products, the per-token scale and the codes.
 // after_x() runs once the first product has read the X stage.
-template <class DT, int MB, int NP, bool PACK, int NV, int MV, class AfterX>
+template <class DT, int MB, int NP, bool PACK, int NV, int MV, bool LF_IN_LDS = FqShape<MB, NP, NV, MV>::LF_LDS,
+          class AfterX>
 __device__ __attribute__((always_inline)) inline void fq_mfma_group(
     const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FqShape<MB, NP>::KS2 + 1],
     const unsigned char* lf_lds,
@@ -644,7 +646,7 @@ __device__ __attribute__((always_inline)) inline void fq_mfma_group(
 #pragma unroll
     for (int s = 0; s < KSL; ++s) {
       V lfv;
-      if constexpr (S::LF_LDS) lfv = *reinterpret_cast<const V*>(lf_lds + (mb * (KS2 + 1) + s) * 1024 + 16 * lane);
+      if constexpr (LF_IN_LDS) lfv = *reinterpret_cast<const V*>(lf_lds + (mb * (KS2 + 1) + s) * 1024 + 16 * lane);
       else lfv = lf[mb][s];
       acc0 = Ops::mfma(zp[0][s], lfv, acc0);
       acc1 = Ops::mfma(zp[1][s], lfv, acc1);
@@ -926,6 +928,137 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
                                               tokens, clip, out_codes, out_scales, lane, tau, q, [] {});
       g = gn;
     }
+  }
+  wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
+}
+
+// ---------------------------------------------------------------------------
+// Few-token kernel (fq_few_kernel): N = 128, M = 16 MB. The decode shapes: a
+// few tokens each take the serial chain of one token, so the chain is split
+// over a workgroup of four waves (one 32-column pair each, the workgroup
+// kernel's per-token work and code path, fq_mfma_group) and the set-up is
+// one round trip: the first token's X (by LDS-DMA, in fragment order) and R
+// and L (16-byte loads, stored row-major into LDS at a 288-byte pitch, so
+// that four consecutive rows start 8 banks apart) are all requested at entry.
+// R's and L's fragments are then gathered with LDS transpose reads into VGPRs
+// (one wave per SIMD leaves room for L's too). Further tokens of a workgroup
+// have their X copied into the other buffer while the current one is used.
+// ---------------------------------------------------------------------------
+template <int MB>
+struct FewShape {
+  static constexpr int M = 16 * MB, N = 128, F = M * N;
+  static constexpr int KS1 = 4, KS2 = MB / 2;
+  static constexpr bool TAIL = (MB & 1) != 0;
+  static constexpr int XFRAGS = MB * KS1;          // 1 KiB X fragments per token
+  static constexpr int XF_PER_WAVE = XFRAGS / 4;   // == MB
+  static constexpr int P = 144;                    // R and L row pitch in elements (288 bytes)
+  static_assert(M <= 128, "L rows fit the staging pitch");
+};
+
+template <class DT, int MB, bool PACK>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+              const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
+              void* __restrict__ out_codes, float* __restrict__ out_scales) {
+  using S = FewShape<MB>;
+  using T = typename DT::T;
+  using V = typename MfmaOps<DT>::V;
+  constexpr int M = S::M, N = S::N, KS1 = S::KS1, KS2 = S::KS2, P = S::P;
+  __shared__ __align__(16) T xbuf0[S::XFRAGS * 512];
+  __shared__ __align__(16) T xbuf1[S::XFRAGS * 512];
+  __shared__ __align__(16) T rst[N * P];
+  __shared__ __align__(16) T lst[M * P];
+  __shared__ float red[1][4][2];
+
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int q = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's 32-column pair
+
+  // LDS-DMA of token tt's X: this wave copies fragments q, q + 4, ...; lane l
+  // of fragment (rb, ks) fetches X[16rb + l%16][32ks + 8(l/16) .. +7].
+  auto issue = [&](int64_t tt, T* stage) {
+    tt = tt < tokens ? tt : tokens - 1;   // past the last token: a valid row, never stored
+    const T* base = x + tt * x_ld + li * N + 8 * lg;
+#pragma unroll
+    for (int i = 0; i < S::XF_PER_WAVE; ++i) {
+      const int f = q + 4 * i;
+      __builtin_amdgcn_global_load_lds((const void*)(base + (f / KS1) * 16 * N + 32 * (f % KS1)),
+                                       (__attribute__((address_space(3))) void*)(stage + f * 512), 16, 0, 0);
+    }
+  };
+
+  int64_t t = blockIdx.x;
+  issue(t, xbuf0);
+  // R (N x N) and L (M x M) as 16-byte chunks, all loads before any store
+  constexpr int RCH = N * N / 8, LCH = M * M / 8;
+  constexpr int RPT = (RCH + 255) / 256, LPT = (LCH + 255) / 256;
+  v4i rtmp[RPT], ltmp[LPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int c = tid + 256 * i;
+    rtmp[i] = reinterpret_cast<const v4i*>(right)[c < RCH ? c : 0];
+  }
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int c = tid + 256 * i;
+    ltmp[i] = reinterpret_cast<const v4i*>(left)[c < LCH ? c : 0];
+  }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int c = tid + 256 * i;   // row c / 16, 8 elements from column 8 (c % 16)
+    if (c < RCH) *reinterpret_cast<v4i*>(rst + (c >> 4) * P + 8 * (c & 15)) = rtmp[i];
+  }
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int c = tid + 256 * i;   // row c / (M / 8)
+    if (c < LCH) *reinterpret_cast<v4i*>(lst + (c / (M / 8)) * P + 8 * (c % (M / 8))) = ltmp[i];
+  }
+  lds_barrier();
+  // R fragments of this pair, rf[h][ks][j] = R[32ks + 8lg + j][n],
+  // n = 32q + 8(li/4) + 4h + li%4: lane l supplies row 32ks + 8lg + l/4 (+4),
+  // columns 32q + 8(l%4) + 4h .. +3, and receives column 32q + 8(l/4) + 4h + l%4.
+  V rf[2][KS1];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks) {
+      const T* at = rst + (32 * ks + 8 * lg + (li >> 2)) * P + 32 * q + 8 * (li & 3) + 4 * h;
+      rf[h][ks] = join_tr16<V>(lds_tr16(at), lds_tr16(at + 4 * P));
+    }
+  // L fragments, lf[mb][s][j] = L[32s + 16(j/4) + 4lg + j%4][16mb + li]; the
+  // zero-padded tail slab (s = KS2, M / 16 odd) has elements 4..7 zero.
+  V lf[MB][KS2 + 1];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int s = 0; s <= KS2; ++s) {
+      const T* at = lst + (32 * s + 4 * lg + (li >> 2)) * P + 16 * mb + 4 * (li & 3);
+      if (s < KS2) lf[mb][s] = join_tr16<V>(lds_tr16(at), lds_tr16(at + 16 * P));
+      else if (S::TAIL) lf[mb][s] = join_tr16<V>(lds_tr16(at), v4s16{0, 0, 0, 0});
+      else lf[mb][s] = V{};
+    }
+
+  // One token per iteration: the next token's X goes into the other buffer,
+  // then this wave's copies of the current one are waited for (copies retire
+  // in order; stores issued in between only make the count stricter) and a
+  // barrier makes every wave's share visible.
+  T* cur = xbuf0;
+  T* nxt = xbuf1;
+  while (t < tokens) {
+    const int64_t tn = t + gridDim.x;
+    if (tn < tokens) {
+      issue(tn, nxt);
+      wait_vmcnt<S::XF_PER_WAVE>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    raw_barrier();
+    fq_mfma_group<DT, MB, 4, PACK, N, M, false>(cur, lf, nullptr, rf, red, t, tokens, clip, out_codes, out_scales,
+                                                lane, 0, q, [] {});
+    lds_barrier();   // every wave is done with cur (and with red) before it is refilled
+    T* tmp = cur;
+    cur = nxt;
+    nxt = tmp;
+    t = tn;
   }
   wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
 }
@@ -1618,6 +1751,18 @@ static int launch_wave(const void* x, int64_t tokens, int64_t x_ld, const void* 
 }
 
 template <class DT, int MB, bool PACK>
+static int launch_few(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right, float clip,
+                      void* out_codes, float* out_scales, hipStream_t stream) {
+  using T = typename DT::T;
+  // one token per workgroup (four waves, one per SIMD); workgroups loop beyond one per CU
+  const int64_t grid = std::min<int64_t>(tokens, (int64_t)device_cu_count());
+  launch((fq_few_kernel<DT, MB, PACK>), dim3((unsigned)grid), dim3(256), 0, stream, reinterpret_cast<const T*>(x),
+         tokens, x_ld, reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), clip, out_codes,
+         out_scales);
+  return QO_OK;
+}
+
+template <class DT, int MB, bool PACK>
 static int launch_duo(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right, float clip,
                       void* out_codes, float* out_scales, hipStream_t stream) {
   using T = typename DT::T;
@@ -1645,6 +1790,12 @@ static bool fq_allow_wave() {
 // QO_ROUTE_FQ_NO_FEW keeps the one-wave and pair kernels at any token count
 // (tests use it to cross-check them against the workgroup kernel on small
 // inputs).
+// Token counts up to which N = 128 shapes take fq_few_kernel (measured, bf16
+// 112 x 128: 16 tokens 7.35 us against 9.34 on the pair kernel, 128 tokens
+// 9.43 against 9.45; 64 x 128 and 96 x 128 also ahead of the workgroup kernel
+// or equal to it).
+constexpr int64_t kFewTokensN128 = 128;
+
 static bool fq_route_few() {
   return !route_off(QO_ROUTE_FQ_NO_FEW);
 }
@@ -1672,6 +1823,17 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
     QO_FQ_WAVE_CASE(2, 1)   // 32 x 32 (hidden 1024)
     QO_FQ_WAVE_CASE(4, 1)   // 64 x 32 (hidden 2048)
 #undef QO_FQ_WAVE_CASE
+  }
+  // N = 128 at decode token counts: the few-token kernel (scale from max |Y| as well)
+  if (N == 128 && clip > 0.f && clip <= 3.4e38f && fq_route_few() && tokens <= kFewTokensN128) {
+#define QO_FQ_FEW_CASE(MB_)                                                                                  \
+    if (M == 16 * (MB_))                                                                                     \
+      return launch_few<DT, MB_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream);
+    QO_FQ_FEW_CASE(7)   // 112 x 128 (hidden 14336)
+    QO_FQ_FEW_CASE(4)   // 64 x 128  (hidden 8192)
+    QO_FQ_FEW_CASE(8)   // 128 x 128 (hidden 16384)
+    QO_FQ_FEW_CASE(6)   // 96 x 128  (hidden 12288)
+#undef QO_FQ_FEW_CASE
   }
   // the pair kernel takes its scale from max |Y| as well
   if (fq_allow_duo() && clip > 0.f && clip <= 3.4e38f && N == 128 && !(few && (M == 64 || M == 96))) {

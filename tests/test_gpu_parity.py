@@ -259,6 +259,27 @@ def test_quantize_pair_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack,
     assert torch.equal(s1, s2) and torch.equal(q1, q2)
 
 
+@pytest.mark.parametrize("pack", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [112, 64, 96, 128])
+@pytest.mark.parametrize("tokens", [1, 16, 37, 128])
+def test_quantize_few_token_kernel_matches_pair_kernel(gpu, tokens, m, dtype, pack, routing):
+    """Up to 128 tokens of N = 128 run the few-token kernel (four waves per
+    token); it uses the pair kernel's fragment layouts and k order, so codes and
+    scales agree bit for bit (zero token included)."""
+    case = wl.quant_case("few", tokens, m, 128, dtype, 0.9, pack, seed=tokens + 3 * m, outlier_frac=0.005,
+                         outlier_scale=30.0)
+    case.x[tokens // 2].zero_()
+    _say(f"few-token vs pair kernel T={tokens} {m}x128 {dtype} pack={pack}")
+    q1, s1 = run_capi_quant(case, gpu)
+    routing.on("FQ_NO_FEW")
+    q2, s2 = run_capi_quant(case, gpu)
+    routing.off("FQ_NO_FEW")
+    assert torch.equal(s1, s2) and torch.equal(q1, q2)
+    if tokens == 16 and m == 112:
+        check_quant(case.x, case.left, case.right, 0.9, pack, q1, s1, f"few-token {m}x128 {dtype}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mn", [(64, 64), (112, 128), (16, 16)])
 def test_quantize_matches_sequential_accumulation_oracle(gpu, dtype, mn, routing):
