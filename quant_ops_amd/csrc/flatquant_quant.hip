@@ -936,7 +936,7 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 // Few-token kernel (fq_few_kernel): N = 128, M = 16 MB. The decode shapes: a
 // few tokens each take the serial chain of one token, so the chain is split
 // over a workgroup of four waves (one 32-column pair each, the workgroup
-// kernel's per-token work and code path, fq_mfma_group) and the set-up is
+// kernel's layouts; fq_few_token) and the set-up is
 // one round trip: the first token's X (by LDS-DMA, in fragment order) and R
 // and L (16-byte loads, stored row-major into LDS at a 288-byte pitch, so
 // that four consecutive rows start 8 banks apart) are all requested at entry.
@@ -955,6 +955,155 @@ struct FewShape {
   static_assert(M <= 128, "L rows fit the staging pitch");
 };
 
+// One token of the few-token kernel on this wave's 32-column pair q, with the
+// workgroup kernel's layouts (X fragments in LDS, R's and L's fragments in
+// VGPRs; see fq_mfma_group) and the pair kernel's epilogue. At one wave per
+// SIMD the MFMAs' result latency is the time, so both products run G row
+// blocks at a time: 2G independent accumulator chains instead of two, each in
+// the same k order (so the results are those of the other kernels, bit for
+// bit). The scale comes from max |Y| (clip > 0): a DPP wave maximum and one
+// LDS exchange across the four waves.
+template <class DT, int MB, bool PACK>
+__device__ __attribute__((always_inline)) inline void fq_few_token(
+    const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FewShape<MB>::KS2 + 1],
+    const typename MfmaOps<DT>::V (&rf)[2][FewShape<MB>::KS1], float* red, int64_t t, float clip,
+    void* __restrict__ out_codes, float* __restrict__ out_scales, int lane, int q) {
+  using S = FewShape<MB>;
+  using T = typename DT::T;
+  using Ops = MfmaOps<DT>;
+  using V = typename Ops::V;
+  using Epi = FqEpi<DT>;
+  constexpr int N = S::N, F = S::F, KS1 = S::KS1, KS2 = S::KS2;
+  constexpr int KSL = KS2 + (S::TAIL ? 1 : 0);
+  const int li = lane & 15, lg = lane >> 4;
+
+  // First product, rounding point 1: zp[h][s][4e + r] = Z[16(2s + e) + 4lg + r][n(h, li)].
+  // G row blocks at a time (2G independent accumulator chains).
+  constexpr int G = 4;
+  V zp[2][KS2 + 1];
+#pragma unroll
+  for (int rb0 = 0; rb0 < MB; rb0 += G) {
+    V a[G][KS1];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int ks = 0; ks < KS1; ++ks)
+        if (rb0 + g < MB) a[g][ks] = *reinterpret_cast<const V*>(xs + (((rb0 + g) * KS1 + ks) * 64 + lane) * 8);
+    v4f c[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) c[g][0] = c[g][1] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (rb0 + g < MB) {
+          c[g][0] = Ops::mfma(a[g][ks], rf[0][ks], c[g][0]);
+          c[g][1] = Ops::mfma(a[g][ks], rf[1][ks], c[g][1]);
+        }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int rb = rb0 + g;
+      if (rb >= MB) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        zp[0][rb >> 1][(rb & 1) * 4 + r] = (T)c[g][0][r];   // MFMA results: no opaque()
+        zp[1][rb >> 1][(rb & 1) * 4 + r] = (T)c[g][1][r];
+        if (S::TAIL && rb == MB - 1) {                      // zero-padded tail slab
+          zp[0][rb >> 1][4 + r] = __builtin_bit_cast(T, (short)0);
+          zp[1][rb >> 1][4 + r] = __builtin_bit_cast(T, (short)0);
+        }
+      }
+    }
+  }
+
+  // Second product, transposed, rounding point 2: lane (li, lg) of block mb
+  // holds Y[16mb + li][32q + 8lg + 4h + r], the pair (h = 0, 1) of nibbles r
+  // and r + 4 of word 4q + lg of that row. G row blocks of Y at a time.
+  uint32_t yp[MB][4];
+  float amax = 0.f;
+#pragma unroll
+  for (int mb0 = 0; mb0 < MB; mb0 += G) {
+    v4f c[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) c[g][0] = c[g][1] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sl = 0; sl < KSL; ++sl)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (mb0 + g < MB) {
+          c[g][0] = Ops::mfma(zp[0][sl], lf[mb0 + g][sl], c[g][0]);
+          c[g][1] = Ops::mfma(zp[1][sl], lf[mb0 + g][sl], c[g][1]);
+        }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (mb0 + g >= MB) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        yp[mb0 + g][r] = Epi::pack_acc(c[g][0][r], c[g][1][r]);
+        amax = fmaxf(fmaxf(amax, fabsf(c[g][0][r])), fabsf(c[g][1][r]));
+      }
+    }
+  }
+  // max |y| over the token: the wave (non-negative floats order like their
+  // bit patterns), then the four waves
+  amax = __builtin_bit_cast(float, wave_max_u32(__builtin_bit_cast(uint32_t, amax)));
+  if (lane == 0) red[q] = amax;
+  lds_barrier();
+  amax = DT::round(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  const float s = fq_scale_abs<DT>(amax, clip);
+  if (q == 0 && lane == 0) out_scales[t] = s;
+  const float rcp = 1.0f / s;
+  if (PACK) {
+    int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + 4 * q + lg;
+    if (s > 0.f) {
+      if constexpr (std::is_same<DT, BF16T>::value) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) orow[(16 * mb + li) * (N / 8)] = (int32_t)Epi::word_u8(yp[mb], rcp);
+      } else if (DT::round(amax * rcp) > 8.5f) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) orow[(16 * mb + li) * (N / 8)] = (int32_t)Epi::template word4<true>(yp[mb], rcp);
+      } else {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) orow[(16 * mb + li) * (N / 8)] = (int32_t)Epi::template word4<false>(yp[mb], rcp);
+      }
+    } else {
+      // scale rounded to 0 (an all-zero fp16 token): the fallback's 0/0 codes
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          w |= (uint32_t)(fq_code_from_quot<true>(DT::round(opaque(Epi::lo(yp[mb][r])) / s)) + 8) << (4 * r);
+          w |= (uint32_t)(fq_code_from_quot<true>(DT::round(opaque(Epi::hi(yp[mb][r])) / s)) + 8) << (4 * r + 16);
+        }
+        orow[(16 * mb + li) * (N / 8)] = (int32_t)w;
+      }
+    }
+  } else {
+    // int8 codes: 8 bytes per row block (columns 32q + 8lg .. + 7)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      uint32_t lo4 = 0, hi4 = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float y0 = Epi::lo(yp[mb][r]), y1 = Epi::hi(yp[mb][r]);
+        int c0, c1;
+        if (s > 0.f) {
+          c0 = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y0 * rcp, -8.0f, 7.0f)));
+          c1 = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y1 * rcp, -8.0f, 7.0f)));
+        } else {
+          c0 = fq_code_from_quot<false>(DT::round(opaque(y0) / s));
+          c1 = fq_code_from_quot<false>(DT::round(opaque(y1) / s));
+        }
+        lo4 |= (uint32_t)(c0 & 0xFF) << (8 * r);
+        hi4 |= (uint32_t)(c1 & 0xFF) << (8 * r);
+      }
+      *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + (16 * mb + li) * N + 32 * q + 8 * lg) =
+          v2i{(int)lo4, (int)hi4};
+    }
+  }
+}
+
 template <class DT, int MB, bool PACK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
@@ -968,7 +1117,7 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   __shared__ __align__(16) T xbuf1[S::XFRAGS * 512];
   __shared__ __align__(16) T rst[N * P];
   __shared__ __align__(16) T lst[M * P];
-  __shared__ float red[1][4][2];
+  __shared__ float red[4];
 
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int q = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's 32-column pair
@@ -1052,8 +1201,7 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
       wait_vmcnt<0>();
     }
     raw_barrier();
-    fq_mfma_group<DT, MB, 4, PACK, N, M, false>(cur, lf, nullptr, rf, red, t, tokens, clip, out_codes, out_scales,
-                                                lane, 0, q, [] {});
+    fq_few_token<DT, MB, PACK>(cur, lf, rf, red, t, clip, out_codes, out_scales, lane, q);
     lds_barrier();   // every wave is done with cur (and with red) before it is refilled
     T* tmp = cur;
     cur = nxt;
