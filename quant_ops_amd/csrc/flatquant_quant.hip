@@ -936,7 +936,7 @@ fq_mfma_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
 // Few-token kernel (fq_few_kernel): N = 128, M = 16 MB. The decode shapes: a
 // few tokens each take the serial chain of one token, so the chain is split
 // over a workgroup of four waves (one 32-column pair each, the workgroup
-// kernel's layouts; fq_few_token) and the set-up is
+// kernel's layouts; few_products) and the set-up is
 // one round trip: the first token's X (by LDS-DMA, in fragment order) and R
 // and L (16-byte loads, stored row-major into LDS at a 288-byte pitch, so
 // that four consecutive rows start 8 banks apart) are all requested at entry.
@@ -955,31 +955,33 @@ struct FewShape {
   static_assert(M <= 128, "L rows fit the staging pitch");
 };
 
-// One token of the few-token kernel on this wave's 32-column pair q, with the
-// workgroup kernel's layouts (X fragments in LDS, R's and L's fragments in
-// VGPRs; see fq_mfma_group) and the pair kernel's epilogue. At one wave per
-// SIMD the MFMAs' result latency is the time, so both products run G row
-// blocks at a time: 2G independent accumulator chains instead of two, each in
-// the same k order (so the results are those of the other kernels, bit for
-// bit). The scale comes from max |Y| (clip > 0): a DPP wave maximum and one
-// LDS exchange across the four waves.
-template <class DT, int MB, bool PACK>
-__device__ __attribute__((always_inline)) inline void fq_few_token(
+// Per-token work of the few-token kernel on this wave's 32-column pair q, with
+// the workgroup kernel's layouts (X fragments in LDS, R's and L's fragments in
+// VGPRs; see fq_mfma_group) and the pair kernel's epilogue, in three parts:
+// the two products (few_products), the scale (few_scale) and the codes
+// (few_codes_packed / few_codes_int8).
+//
+// At one wave per SIMD the MFMAs' result latency is the time, so both products
+// run G row blocks at a time: 2G independent accumulator chains instead of
+// two, each in the same k order (so the results are those of the other
+// kernels, bit for bit). Lane (li, lg) of block mb ends with yp[mb][r], the
+// D-rounded pair (h = 0, 1) Y[16mb + li][32q + 8lg + 4h + r]: nibbles r and
+// r + 4 of word 4q + lg of that row; amax = max |Y| of the wave's raw
+// accumulators.
+template <class DT, int MB>
+__device__ __attribute__((always_inline)) inline void few_products(
     const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FewShape<MB>::KS2 + 1],
-    const typename MfmaOps<DT>::V (&rf)[2][FewShape<MB>::KS1], float* red, int64_t t, float clip,
-    void* __restrict__ out_codes, float* __restrict__ out_scales, int lane, int q) {
+    const typename MfmaOps<DT>::V (&rf)[2][FewShape<MB>::KS1], int lane, uint32_t (&yp)[MB][4], float& amax) {
   using S = FewShape<MB>;
   using T = typename DT::T;
   using Ops = MfmaOps<DT>;
   using V = typename Ops::V;
   using Epi = FqEpi<DT>;
-  constexpr int N = S::N, F = S::F, KS1 = S::KS1, KS2 = S::KS2;
+  constexpr int KS1 = S::KS1, KS2 = S::KS2;
   constexpr int KSL = KS2 + (S::TAIL ? 1 : 0);
-  const int li = lane & 15, lg = lane >> 4;
+  constexpr int G = 4;
 
   // First product, rounding point 1: zp[h][s][4e + r] = Z[16(2s + e) + 4lg + r][n(h, li)].
-  // G row blocks at a time (2G independent accumulator chains).
-  constexpr int G = 4;
   V zp[2][KS2 + 1];
 #pragma unroll
   for (int rb0 = 0; rb0 < MB; rb0 += G) {
@@ -1016,11 +1018,8 @@ __device__ __attribute__((always_inline)) inline void fq_few_token(
     }
   }
 
-  // Second product, transposed, rounding point 2: lane (li, lg) of block mb
-  // holds Y[16mb + li][32q + 8lg + 4h + r], the pair (h = 0, 1) of nibbles r
-  // and r + 4 of word 4q + lg of that row. G row blocks of Y at a time.
-  uint32_t yp[MB][4];
-  float amax = 0.f;
+  // Second product, transposed, rounding point 2, G row blocks of Y at a time.
+  amax = 0.f;
 #pragma unroll
   for (int mb0 = 0; mb0 < MB; mb0 += G) {
     v4f c[G][2];
@@ -1044,63 +1043,78 @@ __device__ __attribute__((always_inline)) inline void fq_few_token(
       }
     }
   }
-  // max |y| over the token: the wave (non-negative floats order like their
-  // bit patterns), then the four waves
+}
+
+// The token's scale from max |Y| (clip > 0): a DPP wave maximum, then one LDS
+// exchange across the four waves (red[4]; the barrier also orders every
+// wave's earlier reads of the X buffer before its refill).
+template <class DT>
+__device__ inline float few_scale(float amax, float* red, int q, int lane, float clip, float& amax_d) {
   amax = __builtin_bit_cast(float, wave_max_u32(__builtin_bit_cast(uint32_t, amax)));
   if (lane == 0) red[q] = amax;
   lds_barrier();
-  amax = DT::round(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
-  const float s = fq_scale_abs<DT>(amax, clip);
-  if (q == 0 && lane == 0) out_scales[t] = s;
+  amax_d = DT::round(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  return fq_scale_abs<DT>(amax_d, clip);
+}
+
+// Packed codes of one token (this lane's word 4q + lg of rows 16mb + li) from
+// rcp = 1 / s, without branches or divisions (either would end the block the
+// products are scheduled with): a scale of 0 (an all-zero fp16 token) stores
+// wrong words here, which few_codes_zero_scale then replaces.
+template <class DT, int MB>
+__device__ inline void few_codes_packed(const uint32_t (&yp)[MB][4], float rcp, int32_t* orow, int li) {
+  using Epi = FqEpi<DT>;
+  constexpr int N = FewShape<MB>::N;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    uint32_t w;
+    if constexpr (std::is_same<DT, BF16T>::value) w = Epi::word_u8(yp[mb], rcp);
+    else w = Epi::template word4<true>(yp[mb], rcp);   // the lower clamp as well: valid for any amax
+    orow[(16 * mb + li) * (N / 8)] = (int32_t)w;
+  }
+}
+
+// Codes of a token whose scale rounded to 0: the fallback's 0/0 codes.
+template <class DT, int MB>
+__device__ inline void few_codes_zero_scale(const uint32_t (&yp)[MB][4], float s, int32_t* orow, int li) {
+  using Epi = FqEpi<DT>;
+  constexpr int N = FewShape<MB>::N;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      w |= (uint32_t)(fq_code_from_quot<true>(DT::round(opaque(Epi::lo(yp[mb][r])) / s)) + 8) << (4 * r);
+      w |= (uint32_t)(fq_code_from_quot<true>(DT::round(opaque(Epi::hi(yp[mb][r])) / s)) + 8) << (4 * r + 16);
+    }
+    orow[(16 * mb + li) * (N / 8)] = (int32_t)w;
+  }
+}
+
+// int8 codes of one token: 8 bytes per row block (columns 32q + 8lg .. + 7).
+template <class DT, int MB>
+__device__ inline void few_codes_int8(const uint32_t (&yp)[MB][4], float s, int8_t* orow, int li) {
+  using Epi = FqEpi<DT>;
+  constexpr int N = FewShape<MB>::N;
   const float rcp = 1.0f / s;
-  if (PACK) {
-    int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + 4 * q + lg;
-    if (s > 0.f) {
-      if constexpr (std::is_same<DT, BF16T>::value) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) orow[(16 * mb + li) * (N / 8)] = (int32_t)Epi::word_u8(yp[mb], rcp);
-      } else if (DT::round(amax * rcp) > 8.5f) {
+  for (int mb = 0; mb < MB; ++mb) {
+    uint32_t lo4 = 0, hi4 = 0;
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) orow[(16 * mb + li) * (N / 8)] = (int32_t)Epi::template word4<true>(yp[mb], rcp);
+    for (int r = 0; r < 4; ++r) {
+      const float y0 = Epi::lo(yp[mb][r]), y1 = Epi::hi(yp[mb][r]);
+      int c0, c1;
+      if (s > 0.f) {
+        c0 = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y0 * rcp, -8.0f, 7.0f)));
+        c1 = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y1 * rcp, -8.0f, 7.0f)));
       } else {
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) orow[(16 * mb + li) * (N / 8)] = (int32_t)Epi::template word4<false>(yp[mb], rcp);
+        c0 = fq_code_from_quot<false>(DT::round(opaque(y0) / s));
+        c1 = fq_code_from_quot<false>(DT::round(opaque(y1) / s));
       }
-    } else {
-      // scale rounded to 0 (an all-zero fp16 token): the fallback's 0/0 codes
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          w |= (uint32_t)(fq_code_from_quot<true>(DT::round(opaque(Epi::lo(yp[mb][r])) / s)) + 8) << (4 * r);
-          w |= (uint32_t)(fq_code_from_quot<true>(DT::round(opaque(Epi::hi(yp[mb][r])) / s)) + 8) << (4 * r + 16);
-        }
-        orow[(16 * mb + li) * (N / 8)] = (int32_t)w;
-      }
+      lo4 |= (uint32_t)(c0 & 0xFF) << (8 * r);
+      hi4 |= (uint32_t)(c1 & 0xFF) << (8 * r);
     }
-  } else {
-    // int8 codes: 8 bytes per row block (columns 32q + 8lg .. + 7)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      uint32_t lo4 = 0, hi4 = 0;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float y0 = Epi::lo(yp[mb][r]), y1 = Epi::hi(yp[mb][r]);
-        int c0, c1;
-        if (s > 0.f) {
-          c0 = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y0 * rcp, -8.0f, 7.0f)));
-          c1 = (int)__builtin_rintf(DT::round(__builtin_amdgcn_fmed3f(y1 * rcp, -8.0f, 7.0f)));
-        } else {
-          c0 = fq_code_from_quot<false>(DT::round(opaque(y0) / s));
-          c1 = fq_code_from_quot<false>(DT::round(opaque(y1) / s));
-        }
-        lo4 |= (uint32_t)(c0 & 0xFF) << (8 * r);
-        hi4 |= (uint32_t)(c1 & 0xFF) << (8 * r);
-      }
-      *reinterpret_cast<v2i*>(reinterpret_cast<int8_t*>(out_codes) + t * F + (16 * mb + li) * N + 32 * q + 8 * lg) =
-          v2i{(int)lo4, (int)hi4};
-    }
+    *reinterpret_cast<v2i*>(orow + (16 * mb + li) * N) = v2i{(int)lo4, (int)hi4};
   }
 }
 
@@ -1123,15 +1137,19 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   const int q = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's 32-column pair
 
   // LDS-DMA of token tt's X: this wave copies fragments q, q + 4, ...; lane l
-  // of fragment (rb, ks) fetches X[16rb + l%16][32ks + 8(l/16) .. +7].
+  // of fragment (rb, ks) fetches X[16rb + l%16][32ks + 8(l/16) .. +7]. The
+  // copies are issued as inline assembly (dma16): the compiler then adds no
+  // wait of its own for them (with the builtin it waits for every outstanding
+  // load before the next LDS read, which would also wait for the next token's
+  // copy); the loop below waits for them explicitly.
   auto issue = [&](int64_t tt, T* stage) {
     tt = tt < tokens ? tt : tokens - 1;   // past the last token: a valid row, never stored
     const T* base = x + tt * x_ld + li * N + 8 * lg;
+    const uint32_t lbase = lds_addr(stage);
 #pragma unroll
     for (int i = 0; i < S::XF_PER_WAVE; ++i) {
       const int f = q + 4 * i;
-      __builtin_amdgcn_global_load_lds((const void*)(base + (f / KS1) * 16 * N + 32 * (f % KS1)),
-                                       (__attribute__((address_space(3))) void*)(stage + f * 512), 16, 0, 0);
+      dma16(base + (f / KS1) * 16 * N + 32 * (f % KS1), lbase + f * 1024);
     }
   };
 
@@ -1189,11 +1207,17 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   // One token per iteration: the next token's X goes into the other buffer,
   // then this wave's copies of the current one are waited for (copies retire
   // in order; stores issued in between only make the count stricter) and a
-  // barrier makes every wave's share visible.
+  // barrier makes every wave's share visible. The barrier inside few_scale
+  // comes after every wave's reads of the current buffer, so the buffer can be
+  // refilled in the next iteration.
+  //
+  // Packed codes are software-pipelined: token i's codes (VALU work) are
+  // computed in the same block as token i + 1's products (MFMA work), which
+  // leaves the two to be interleaved, since at one wave per SIMD nothing else
+  // hides either.
   T* cur = xbuf0;
   T* nxt = xbuf1;
-  while (t < tokens) {
-    const int64_t tn = t + gridDim.x;
+  auto next_x = [&](int64_t tn) {
     if (tn < tokens) {
       issue(tn, nxt);
       wait_vmcnt<S::XF_PER_WAVE>();
@@ -1201,12 +1225,65 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
       wait_vmcnt<0>();
     }
     raw_barrier();
-    fq_few_token<DT, MB, PACK>(cur, lf, rf, red, t, clip, out_codes, out_scales, lane, q);
-    lds_barrier();   // every wave is done with cur (and with red) before it is refilled
-    T* tmp = cur;
-    cur = nxt;
-    nxt = tmp;
-    t = tn;
+  };
+  if constexpr (PACK) {
+    uint32_t ypp[MB][4];
+    float sp, rcpp, amax_d;
+    int64_t tp = t;
+    {
+      const int64_t tn = t + gridDim.x;
+      next_x(tn);
+      float amax;
+      few_products<DT, MB>(cur, lf, rf, lane, ypp, amax);
+      sp = few_scale<DT>(amax, red, q, lane, clip, amax_d);
+      rcpp = 1.0f / sp;
+      if (q == 0 && lane == 0) out_scales[t] = sp;
+      T* tmp = cur;
+      cur = nxt;
+      nxt = tmp;
+      t = tn;
+    }
+    while (t < tokens) {
+      const int64_t tn = t + gridDim.x;
+      next_x(tn);
+      uint32_t yp[MB][4];
+      float amax;
+      few_products<DT, MB>(cur, lf, rf, lane, yp, amax);
+      int32_t* orowp = reinterpret_cast<int32_t*>(out_codes) + tp * (S::F / 8) + 4 * q + lg;
+      few_codes_packed<DT, MB>(ypp, rcpp, orowp, li);
+      const float s = few_scale<DT>(amax, red, q, lane, clip, amax_d);
+      if (q == 0 && lane == 0) out_scales[t] = s;
+      if (!(sp > 0.f)) few_codes_zero_scale<DT, MB>(ypp, sp, orowp, li);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ypp[mb][r] = yp[mb][r];
+      sp = s;
+      rcpp = 1.0f / s;
+      tp = t;
+      T* tmp = cur;
+      cur = nxt;
+      nxt = tmp;
+      t = tn;
+    }
+    int32_t* orowp = reinterpret_cast<int32_t*>(out_codes) + tp * (S::F / 8) + 4 * q + lg;
+    few_codes_packed<DT, MB>(ypp, rcpp, orowp, li);
+    if (!(sp > 0.f)) few_codes_zero_scale<DT, MB>(ypp, sp, orowp, li);
+  } else {
+    while (t < tokens) {
+      const int64_t tn = t + gridDim.x;
+      next_x(tn);
+      uint32_t yp[MB][4];
+      float amax, amax_d;
+      few_products<DT, MB>(cur, lf, rf, lane, yp, amax);
+      const float s = few_scale<DT>(amax, red, q, lane, clip, amax_d);
+      if (q == 0 && lane == 0) out_scales[t] = s;
+      few_codes_int8<DT, MB>(yp, s, reinterpret_cast<int8_t*>(out_codes) + t * S::F + 32 * q + 8 * lg, li);
+      T* tmp = cur;
+      cur = nxt;
+      nxt = tmp;
+      t = tn;
+    }
   }
   wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
 }
@@ -1938,10 +2015,11 @@ static bool fq_allow_wave() {
 // QO_ROUTE_FQ_NO_FEW keeps the one-wave and pair kernels at any token count
 // (tests use it to cross-check them against the workgroup kernel on small
 // inputs).
-// Token counts up to which N = 128 shapes take fq_few_kernel (measured, bf16
-// 112 x 128: 16 tokens 7.35 us against 9.34 on the pair kernel, 128 tokens
-// 9.43 against 9.45; 64 x 128 and 96 x 128 also ahead of the workgroup kernel
-// or equal to it).
+// N = 128 shapes take fq_few_kernel at any token count except 64 x 128, where
+// the pair kernel is faster beyond kFewTokensN128 tokens (measured, 8192
+// tokens bf16: 64 x 128 50.1 vs 46.6 us on the pair kernel; 96 x 128 72.4 vs
+// 73.4, 112 x 128 88.3 vs 88.6, fp16 128 x 128 94.7 vs 96.6; 112 x 128 at 256
+// tokens 7.4 vs 10.2, at 4096 tokens 46.4 vs 49.2).
 constexpr int64_t kFewTokensN128 = 128;
 
 static bool fq_route_few() {
@@ -1973,7 +2051,7 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
 #undef QO_FQ_WAVE_CASE
   }
   // N = 128 at decode token counts: the few-token kernel (scale from max |Y| as well)
-  if (N == 128 && clip > 0.f && clip <= 3.4e38f && fq_route_few() && tokens <= kFewTokensN128) {
+  if (N == 128 && clip > 0.f && clip <= 3.4e38f && fq_route_few() && (tokens <= kFewTokensN128 || M != 64)) {
 #define QO_FQ_FEW_CASE(MB_)                                                                                  \
     if (M == 16 * (MB_))                                                                                     \
       return launch_few<DT, MB_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream);

@@ -262,14 +262,16 @@ def test_quantize_pair_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack,
 @pytest.mark.parametrize("pack", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m", [112, 64, 96, 128])
-@pytest.mark.parametrize("tokens", [1, 16, 37, 128])
+@pytest.mark.parametrize("tokens", [1, 16, 37, 128, 600, 1030])
 def test_quantize_few_token_kernel_matches_pair_kernel(gpu, tokens, m, dtype, pack, routing):
-    """Up to 128 tokens of N = 128 run the few-token kernel (four waves per
-    token); it uses the pair kernel's fragment layouts and k order, so codes and
-    scales agree bit for bit (zero token included)."""
+    """N = 128 runs the few-token kernel (four waves per token; 64 x 128 up to
+    128 tokens); it uses the pair kernel's fragment layouts and k order, so
+    codes and scales agree bit for bit (zero token included). 600 and 1030
+    tokens make workgroups loop over several tokens (the pipelined codes)."""
     case = wl.quant_case("few", tokens, m, 128, dtype, 0.9, pack, seed=tokens + 3 * m, outlier_frac=0.005,
                          outlier_scale=30.0)
     case.x[tokens // 2].zero_()
+    case.x[-1].zero_()          # a zero token last: its codes are stored after the loop
     _say(f"few-token vs pair kernel T={tokens} {m}x128 {dtype} pack={pack}")
     q1, s1 = run_capi_quant(case, gpu)
     routing.on("FQ_NO_FEW")
