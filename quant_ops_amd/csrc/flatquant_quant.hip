@@ -968,9 +968,10 @@ struct FewShape {
 // D-rounded pair (h = 0, 1) Y[16mb + li][32q + 8lg + 4h + r]: nibbles r and
 // r + 4 of word 4q + lg of that row; amax = max |Y| of the wave's raw
 // accumulators.
-template <class DT, int MB>
+// lfrag(mb, s) returns L's fragment (mb, s) (from VGPRs or LDS).
+template <class DT, int MB, class LFrag>
 __device__ __attribute__((always_inline)) inline void few_products(
-    const typename DT::T* __restrict__ xs, const typename MfmaOps<DT>::V (&lf)[MB][FewShape<MB>::KS2 + 1],
+    const typename DT::T* __restrict__ xs, LFrag&& lfrag,
     const typename MfmaOps<DT>::V (&rf)[2][FewShape<MB>::KS1], int lane, uint32_t (&yp)[MB][4], float& amax) {
   using S = FewShape<MB>;
   using T = typename DT::T;
@@ -1030,8 +1031,9 @@ __device__ __attribute__((always_inline)) inline void few_products(
 #pragma unroll
       for (int g = 0; g < G; ++g)
         if (mb0 + g < MB) {
-          c[g][0] = Ops::mfma(zp[0][sl], lf[mb0 + g][sl], c[g][0]);
-          c[g][1] = Ops::mfma(zp[1][sl], lf[mb0 + g][sl], c[g][1]);
+          const V lv = lfrag(mb0 + g, sl);
+          c[g][0] = Ops::mfma(zp[0][sl], lv, c[g][0]);
+          c[g][1] = Ops::mfma(zp[1][sl], lv, c[g][1]);
         }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -1118,8 +1120,12 @@ __device__ inline void few_codes_int8(const uint32_t (&yp)[MB][4], float s, int8
   }
 }
 
-template <class DT, int MB, bool PACK>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// SLOTS = 1: one token at a time per workgroup, L's fragments in VGPRs (one
+// wave per SIMD). SLOTS = 2 (many tokens): two tokens at a time, four waves
+// each (two waves per SIMD, so one token's MFMA or VALU work can run while the
+// other waits), L's fragments in LDS, shared by all eight waves.
+template <class DT, int MB, bool PACK, int SLOTS>
+__global__ void __launch_bounds__(256 * SLOTS) __attribute__((amdgpu_waves_per_eu(SLOTS, SLOTS)))
 fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
               const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
               void* __restrict__ out_codes, float* __restrict__ out_scales) {
@@ -1127,14 +1133,24 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   using T = typename DT::T;
   using V = typename MfmaOps<DT>::V;
   constexpr int M = S::M, N = S::N, KS1 = S::KS1, KS2 = S::KS2, P = S::P;
-  __shared__ __align__(16) T xbuf0[S::XFRAGS * 512];
-  __shared__ __align__(16) T xbuf1[S::XFRAGS * 512];
-  __shared__ __align__(16) T rst[N * P];
-  __shared__ __align__(16) T lst[M * P];
-  __shared__ float red[4];
+  constexpr int XE = S::XFRAGS * 512;           // elements of one token's X buffer
+  constexpr int LF_FRAGS = MB * (KS2 + 1);
+  // X buffer b of slot p at xb + (b SLOTS + p) XE. With one slot R and L are
+  // staged in arrays of their own; with two, R and then L go through the two
+  // slots' second buffers (free at set-up) and L's fragments get an LDS array.
+  constexpr int STAGE_E = SLOTS == 1 ? (N + M) * P : 8;
+  __shared__ __align__(16) T xb[2 * SLOTS * XE];
+  __shared__ __align__(16) T stage_arr[STAGE_E];
+  __shared__ __align__(16) unsigned char lfs[SLOTS == 1 ? 16 : LF_FRAGS * 1024];
+  __shared__ float red[SLOTS][4];
+  static_assert(SLOTS == 1 || (N * P <= 2 * XE && M * P <= 2 * XE), "staging fits two X buffers");
 
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-  const int q = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's 32-column pair
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = wave & 3;                 // this wave's 32-column pair
+  const int p = SLOTS == 1 ? 0 : wave >> 2;   // its token slot
+  T* const rst = SLOTS == 1 ? stage_arr : xb + SLOTS * XE;   // the second buffers
+  T* const lst = SLOTS == 1 ? stage_arr + N * P : xb + SLOTS * XE;
 
   // LDS-DMA of token tt's X: this wave copies fragments q, q + 4, ...; lane l
   // of fragment (rb, ks) fetches X[16rb + l%16][32ks + 8(l/16) .. +7]. The
@@ -1153,32 +1169,41 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     }
   };
 
-  int64_t t = blockIdx.x;
-  issue(t, xbuf0);
+  // tokens of slot p: blockIdx SLOTS + p, then every SLOTS grid further on
+  const int64_t stride = (int64_t)gridDim.x * SLOTS;
+  int64_t t = (int64_t)blockIdx.x * SLOTS + p;
+  const int64_t t_slot0 = (int64_t)blockIdx.x * SLOTS;   // slot 0 has at least as many tokens as slot 1
+  T* cur = xb + p * XE;
+  T* nxt = xb + (SLOTS + p) * XE;
+  issue(t, cur);
   // R (N x N) and L (M x M) as 16-byte chunks, all loads before any store
+  constexpr int NT = 256 * SLOTS;
   constexpr int RCH = N * N / 8, LCH = M * M / 8;
-  constexpr int RPT = (RCH + 255) / 256, LPT = (LCH + 255) / 256;
+  constexpr int RPT = (RCH + NT - 1) / NT, LPT = (LCH + NT - 1) / NT;
   v4i rtmp[RPT], ltmp[LPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
-    const int c = tid + 256 * i;
+    const int c = tid + NT * i;
     rtmp[i] = reinterpret_cast<const v4i*>(right)[c < RCH ? c : 0];
   }
 #pragma unroll
   for (int i = 0; i < LPT; ++i) {
-    const int c = tid + 256 * i;
+    const int c = tid + NT * i;
     ltmp[i] = reinterpret_cast<const v4i*>(left)[c < LCH ? c : 0];
   }
+  auto store_l = [&]() {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + NT * i;   // row c / (M / 8)
+      if (c < LCH) *reinterpret_cast<v4i*>(lst + (c / (M / 8)) * P + 8 * (c % (M / 8))) = ltmp[i];
+    }
+  };
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
-    const int c = tid + 256 * i;   // row c / 16, 8 elements from column 8 (c % 16)
+    const int c = tid + NT * i;   // row c / 16, 8 elements from column 8 (c % 16)
     if (c < RCH) *reinterpret_cast<v4i*>(rst + (c >> 4) * P + 8 * (c & 15)) = rtmp[i];
   }
-#pragma unroll
-  for (int i = 0; i < LPT; ++i) {
-    const int c = tid + 256 * i;   // row c / (M / 8)
-    if (c < LCH) *reinterpret_cast<v4i*>(lst + (c / (M / 8)) * P + 8 * (c % (M / 8))) = ltmp[i];
-  }
+  if constexpr (SLOTS == 1) store_l();
   lds_barrier();
   // R fragments of this pair, rf[h][ks][j] = R[32ks + 8lg + j][n],
   // n = 32q + 8(li/4) + 4h + li%4: lane l supplies row 32ks + 8lg + l/4 (+4),
@@ -1193,32 +1218,45 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     }
   // L fragments, lf[mb][s][j] = L[32s + 16(j/4) + 4lg + j%4][16mb + li]; the
   // zero-padded tail slab (s = KS2, M / 16 odd) has elements 4..7 zero.
-  V lf[MB][KS2 + 1];
+  auto lgather = [&](int mb, int sl) -> V {
+    const T* at = lst + (32 * sl + 4 * lg + (li >> 2)) * P + 16 * mb + 4 * (li & 3);
+    if (sl < KS2) return join_tr16<V>(lds_tr16(at), lds_tr16(at + 16 * P));
+    if (S::TAIL) return join_tr16<V>(lds_tr16(at), v4s16{0, 0, 0, 0});
+    return V{};
+  };
+  V lf[SLOTS == 1 ? MB : 1][KS2 + 1];
+  if constexpr (SLOTS == 1) {
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int s = 0; s <= KS2; ++s) {
-      const T* at = lst + (32 * s + 4 * lg + (li >> 2)) * P + 16 * mb + 4 * (li & 3);
-      if (s < KS2) lf[mb][s] = join_tr16<V>(lds_tr16(at), lds_tr16(at + 16 * P));
-      else if (S::TAIL) lf[mb][s] = join_tr16<V>(lds_tr16(at), v4s16{0, 0, 0, 0});
-      else lf[mb][s] = V{};
-    }
+      for (int sl = 0; sl <= KS2; ++sl) lf[mb][sl] = lgather(mb, sl);
+  } else {
+    lds_barrier();   // every wave holds R's fragments: L may overwrite R's staged rows
+    store_l();
+    lds_barrier();
+#pragma unroll 1
+    for (int fr = wave; fr < LF_FRAGS; fr += 4 * SLOTS)
+      *reinterpret_cast<V*>(lfs + fr * 1024 + 16 * lane) = lgather(fr / (KS2 + 1), fr % (KS2 + 1));
+    lds_barrier();   // L's fragments written; the staging buffers are free for X
+  }
+  auto lfrag = [&](int mb, int sl) -> V {
+    if constexpr (SLOTS == 1) return lf[mb][sl];
+    else return *reinterpret_cast<const V*>(lfs + (mb * (KS2 + 1) + sl) * 1024 + 16 * lane);
+  };
 
-  // One token per iteration: the next token's X goes into the other buffer,
-  // then this wave's copies of the current one are waited for (copies retire
-  // in order; stores issued in between only make the count stricter) and a
-  // barrier makes every wave's share visible. The barrier inside few_scale
-  // comes after every wave's reads of the current buffer, so the buffer can be
-  // refilled in the next iteration.
+  // One token per slot and iteration: the next token's X goes into the other
+  // buffer, then this wave's copies of the current one are waited for (copies
+  // retire in order; stores issued in between only make the count stricter)
+  // and a barrier makes every wave's share visible. The barrier inside
+  // few_scale comes after every wave's reads of the current buffer, so the
+  // buffer can be refilled in the next iteration. Both slots run the same
+  // number of iterations (slot 1's past the last token compute on the last
+  // token and store nothing), so they meet at every barrier.
   //
   // Packed codes are software-pipelined: token i's codes (VALU work) are
-  // computed in the same block as token i + 1's products (MFMA work), which
-  // leaves the two to be interleaved, since at one wave per SIMD nothing else
-  // hides either.
-  T* cur = xbuf0;
-  T* nxt = xbuf1;
+  // computed in the iteration of token i + 1's products (MFMA work).
   auto next_x = [&](int64_t tn) {
-    if (tn < tokens) {
+    if (tn < tokens + (SLOTS - 1)) {   // slot 1 copies (a valid row) as long as slot 0 has a token
       issue(tn, nxt);
       wait_vmcnt<S::XF_PER_WAVE>();
     } else {
@@ -1226,34 +1264,35 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     }
     raw_barrier();
   };
+  float* const red_p = red[p];
   if constexpr (PACK) {
     uint32_t ypp[MB][4];
     float sp, rcpp, amax_d;
     int64_t tp = t;
     {
-      const int64_t tn = t + gridDim.x;
+      const int64_t tn = t + stride;
       next_x(tn);
       float amax;
-      few_products<DT, MB>(cur, lf, rf, lane, ypp, amax);
-      sp = few_scale<DT>(amax, red, q, lane, clip, amax_d);
+      few_products<DT, MB>(cur, lfrag, rf, lane, ypp, amax);
+      sp = few_scale<DT>(amax, red_p, q, lane, clip, amax_d);
       rcpp = 1.0f / sp;
-      if (q == 0 && lane == 0) out_scales[t] = sp;
+      if (q == 0 && lane == 0 && t < tokens) out_scales[t] = sp;
       T* tmp = cur;
       cur = nxt;
       nxt = tmp;
       t = tn;
     }
-    while (t < tokens) {
-      const int64_t tn = t + gridDim.x;
+    for (int64_t t0 = t_slot0 + stride; t0 < tokens; t0 += stride) {
+      const int64_t tn = t + stride;
       next_x(tn);
       uint32_t yp[MB][4];
       float amax;
-      few_products<DT, MB>(cur, lf, rf, lane, yp, amax);
+      few_products<DT, MB>(cur, lfrag, rf, lane, yp, amax);
       int32_t* orowp = reinterpret_cast<int32_t*>(out_codes) + tp * (S::F / 8) + 4 * q + lg;
-      few_codes_packed<DT, MB>(ypp, rcpp, orowp, li);
-      const float s = few_scale<DT>(amax, red, q, lane, clip, amax_d);
-      if (q == 0 && lane == 0) out_scales[t] = s;
-      if (!(sp > 0.f)) few_codes_zero_scale<DT, MB>(ypp, sp, orowp, li);
+      if (tp < tokens) few_codes_packed<DT, MB>(ypp, rcpp, orowp, li);
+      const float s = few_scale<DT>(amax, red_p, q, lane, clip, amax_d);
+      if (q == 0 && lane == 0 && t < tokens) out_scales[t] = s;
+      if (tp < tokens && !(sp > 0.f)) few_codes_zero_scale<DT, MB>(ypp, sp, orowp, li);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -1267,18 +1306,22 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
       t = tn;
     }
     int32_t* orowp = reinterpret_cast<int32_t*>(out_codes) + tp * (S::F / 8) + 4 * q + lg;
-    few_codes_packed<DT, MB>(ypp, rcpp, orowp, li);
-    if (!(sp > 0.f)) few_codes_zero_scale<DT, MB>(ypp, sp, orowp, li);
+    if (tp < tokens) {
+      few_codes_packed<DT, MB>(ypp, rcpp, orowp, li);
+      if (!(sp > 0.f)) few_codes_zero_scale<DT, MB>(ypp, sp, orowp, li);
+    }
   } else {
-    while (t < tokens) {
-      const int64_t tn = t + gridDim.x;
+    for (int64_t t0 = t_slot0; t0 < tokens; t0 += stride) {
+      const int64_t tn = t + stride;
       next_x(tn);
       uint32_t yp[MB][4];
       float amax, amax_d;
-      few_products<DT, MB>(cur, lf, rf, lane, yp, amax);
-      const float s = few_scale<DT>(amax, red, q, lane, clip, amax_d);
-      if (q == 0 && lane == 0) out_scales[t] = s;
-      few_codes_int8<DT, MB>(yp, s, reinterpret_cast<int8_t*>(out_codes) + t * S::F + 32 * q + 8 * lg, li);
+      few_products<DT, MB>(cur, lfrag, rf, lane, yp, amax);
+      const float s = few_scale<DT>(amax, red_p, q, lane, clip, amax_d);
+      if (t < tokens) {
+        if (q == 0 && lane == 0) out_scales[t] = s;
+        few_codes_int8<DT, MB>(yp, s, reinterpret_cast<int8_t*>(out_codes) + t * S::F + 32 * q + 8 * lg, li);
+      }
       T* tmp = cur;
       cur = nxt;
       nxt = tmp;
@@ -1975,13 +2018,37 @@ static int launch_wave(const void* x, int64_t tokens, int64_t x_ld, const void* 
   return QO_OK;
 }
 
+// N = 128 shapes take fq_few_kernel at any token count except 64 x 128, where
+// the pair kernel is faster beyond kFewTokensN128 tokens (measured, 8192
+// tokens bf16: 64 x 128 50.1 vs 46.6 us on the pair kernel; 96 x 128 72.4 vs
+// 73.4, 112 x 128 88.3 vs 88.6, fp16 128 x 128 94.7 vs 96.6; 112 x 128 at 256
+// tokens 7.4 vs 10.2, at 4096 tokens 46.4 vs 49.2).
+constexpr int64_t kFewTokensN128 = 128;
+// Tokens per CU above which 96 x 128 keeps two tokens in flight per workgroup
+// (8192 tokens bf16: 72.8 us with two slots vs 75.7 with one). 112 x 128 stays
+// on one slot, which is faster there (8192 tokens 89.3 vs 92.1 us, 4096 tokens
+// 48.9 vs 51.4, 1024 tokens 17.6 vs 20.3); 64 x 128 and 128 x 128 do not fit
+// two slots' buffers beside L's fragments.
+constexpr int64_t kFewTwoSlots = 2;
+
 template <class DT, int MB, bool PACK>
 static int launch_few(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right, float clip,
                       void* out_codes, float* out_scales, hipStream_t stream) {
   using T = typename DT::T;
-  // one token per workgroup (four waves, one per SIMD); workgroups loop beyond one per CU
-  const int64_t grid = std::min<int64_t>(tokens, (int64_t)device_cu_count());
-  launch((fq_few_kernel<DT, MB, PACK>), dim3((unsigned)grid), dim3(256), 0, stream, reinterpret_cast<const T*>(x),
+  const int64_t cus = device_cu_count();
+  if constexpr (MB == 6) {
+    if (tokens > kFewTwoSlots * cus) {
+      // two tokens at a time per workgroup (eight waves, two per SIMD), one workgroup per CU
+      const int64_t grid = std::min<int64_t>((tokens + 1) / 2, cus);
+      launch((fq_few_kernel<DT, MB, PACK, 2>), dim3((unsigned)grid), dim3(512), 0, stream,
+             reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
+             reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
+      return QO_OK;
+    }
+  }
+  // one token at a time per workgroup (four waves, one per SIMD); workgroups loop beyond one per CU
+  const int64_t grid = std::min<int64_t>(tokens, cus);
+  launch((fq_few_kernel<DT, MB, PACK, 1>), dim3((unsigned)grid), dim3(256), 0, stream, reinterpret_cast<const T*>(x),
          tokens, x_ld, reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), clip, out_codes,
          out_scales);
   return QO_OK;
@@ -2015,12 +2082,6 @@ static bool fq_allow_wave() {
 // QO_ROUTE_FQ_NO_FEW keeps the one-wave and pair kernels at any token count
 // (tests use it to cross-check them against the workgroup kernel on small
 // inputs).
-// N = 128 shapes take fq_few_kernel at any token count except 64 x 128, where
-// the pair kernel is faster beyond kFewTokensN128 tokens (measured, 8192
-// tokens bf16: 64 x 128 50.1 vs 46.6 us on the pair kernel; 96 x 128 72.4 vs
-// 73.4, 112 x 128 88.3 vs 88.6, fp16 128 x 128 94.7 vs 96.6; 112 x 128 at 256
-// tokens 7.4 vs 10.2, at 4096 tokens 46.4 vs 49.2).
-constexpr int64_t kFewTokensN128 = 128;
 
 static bool fq_route_few() {
   return !route_off(QO_ROUTE_FQ_NO_FEW);
