@@ -13,9 +13,10 @@ bound) and ``cpu_baseline`` (this repo's CPU restatement of the reference
 fallback, timed on the host cores on a bounded sample, in the same unit):
 
 * ``gemm_cfg4`` (the headline), ``quantize_cfg2``, ``quantize_cfg3``;
-* ``linear_cfg5_T16`` and ``linear_cfg5_T4096``: quantize + GEMM as one step,
-  and each kernel timed alone; T = 16 is judged on the HBM rate of the GEMM,
-  whose bytes are the 29.4 MB weight read;
+* ``linear_cfg5_T16`` and ``linear_cfg5_T4096``: one call of the linear layer
+  (qo_w4a4_linear: quantize, then the GEMM against W.t()) as the step, and
+  each kernel timed alone; T = 16 is judged on the HBM rate of the GEMM, whose
+  bytes are the 29.4 MB weight read;
 * ``quantize_cfg1``: the fp32 CPU-plumbing config, with the round-trip errors
   of ``dequantize_int4`` for the CPU fallback and for the GPU kernel.
 
@@ -204,16 +205,19 @@ def linear_inputs(torch, tokens):
 
 
 def bench_linear(torch, tokens, steps, warmup, dev):
-    """Config 5 at ``tokens``: the step (quantize, then the GEMM against W.t() with
-    bf16 output) and each of its two kernels timed alone, every buffer rotated
-    (X, W, codes, scales, output)."""
+    """Config 5 at ``tokens``: the step is one call of the linear layer's entry
+    point (qo_w4a4_linear: quantize, then the GEMM against W.t() with bf16
+    output), every buffer rotated (X, W, codes, scales, output); beside it
+    each of the two kernels timed alone."""
     from quant_ops_amd import capi
 
     x_h, L_h, R_h, w_h, sw_h = linear_inputs(torch, tokens)
     L, R, sw = L_h.to(dev), R_h.to(dev), sw_h.to(dev)
     w_bytes = LIN_N * LIN_K // 2
-    q_bytes = tokens * LIN_K * 2 + tokens * LIN_K // 2 + tokens * 4 + 2 * (LIN_M ** 2 + LIN_NT ** 2)
+    q_bytes = _lin_q_bytes(tokens)
     g_bytes = w_bytes + tokens * LIN_K // 2 + tokens * 4 + LIN_N * 2 + tokens * LIN_N * 2
+    # one step from HBM: X, L, R in, codes and scales out, W and its scales in, output out
+    s_bytes = q_bytes + w_bytes + LIN_N * 2 + tokens * LIN_N * 2
     per_set = tokens * LIN_K * 2 + w_bytes + tokens * LIN_K // 2 + tokens * 4 + tokens * LIN_N * 2
     nbuf = _nsets(per_set, steps)
     x0, w0 = x_h.to(dev), w_h.to(dev)
@@ -229,19 +233,23 @@ def bench_linear(torch, tokens, steps, warmup, dev):
     def gemm(j):
         capi.int4_gemm(codes[j], ws[j].t(), scales[j], sw, out=outs[j])
 
+    def step(j):
+        capi.w4a4_linear(xs[j], L, R, ws[j], sw, 0.9, out=outs[j], codes=codes[j], scales=scales[j])
+
     for j in range(nbuf):      # codes of every set, for the GEMM timed alone
         quant(j)
     torch.cuda.synchronize()
     ms_q, _ = _time_graph(torch, lambda i: quant(i % nbuf), steps, warmup)
     ms_g, _ = _time_graph(torch, lambda i: gemm(i % nbuf), steps, warmup)
-    ms_s, wall = _time_graph(torch, lambda i: (quant(i % nbuf), gemm(i % nbuf)), steps, warmup)
+    ms_s, wall = _time_graph(torch, lambda i: step(i % nbuf), steps, warmup)
     t_q, t_g, t_s = (ms / 1e3 / steps for ms in (ms_q, ms_g, ms_s))
     ops = 2 * tokens * LIN_N * LIN_K
     gemm_gbs = g_bytes / t_g / 1e9
     out = {
         "workload": f"cfg5_w4a4_linear_down_proj_T{tokens}", "tokens": tokens, "K": LIN_K, "N": LIN_N,
-        "buffers_rotated": nbuf, "us_per_step": t_s * 1e6, "quantize_us": t_q * 1e6, "gemm_us": t_g * 1e6,
-        "ops_per_step": ops, "TOPS": ops / t_s / 1e12, "gemm_TOPS": ops / t_g / 1e12,
+        "buffers_rotated": nbuf, "us_per_step": t_s * 1e6, "quantize_us": t_q * 1e6,
+        "gemm_us": t_g * 1e6, "ops_per_step": ops, "TOPS": ops / t_s / 1e12, "gemm_TOPS": ops / t_g / 1e12,
+        "step_bytes": s_bytes, "step_GBps": s_bytes / t_s / 1e9,
         "quantize_bytes": q_bytes, "quantize_GBps": q_bytes / t_q / 1e9,
         "gemm_bytes": g_bytes, "gemm_GBps": gemm_gbs, "weight_bytes": w_bytes,
         "weight_GBps_gemm": w_bytes / t_g / 1e9, "weight_GBps_step": w_bytes / t_s / 1e9, "wall_s": wall,

@@ -147,6 +147,37 @@ int qo_int4_gemm_bias(const int32_t* a, int64_t lda,
                       int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
+ * W4A4 FlatQuant linear layer: per-token dynamic quantization of x with the
+ * Kronecker transform (as qo_flatquant_quantize, packed codes), then the int4
+ * GEMM against the packed weight with per-token x per-channel scales, output
+ * in x's dtype, then + bias (as qo_int4_gemm_bias): those two calls on one
+ * stream, so the output equals theirs bit for bit.
+ *
+ * Replaces the GPU path of AscendW4A4FlatQuantDynamicLinearMethod.apply
+ * (w4a4_flatquant_dynamic.py:168-266), which runs the quantize operator and
+ * then the GEMM against weight.t().
+ *
+ *   x             [tokens, M*N] of x_dtype (F32, F16, BF16), row stride x_ld
+ *   left, right   [M, M], [N, N] of x_dtype, contiguous
+ *   weight        int32 [out_features, M*N/8] (packed codes, one row per
+ *                 output channel), row stride weight_ld words
+ *   weight_scale  [out_features] of weight_scale_dtype (F32, F16, BF16)
+ *   bias          NULL or [out_features] of x_dtype
+ *   codes         int32 [tokens, M*N/8], contiguous: the activation codes
+ *   act_scales    float32 [tokens]: the activation scales
+ *   out           [tokens, out_features] of x_dtype, row stride out_ld
+ *
+ * Errors: those of qo_flatquant_quantize and qo_int4_gemm; QO_ERR_SHAPE if
+ * M*N % 8 != 0, out_features < 1 or a stride is below its row length.
+ */
+int qo_w4a4_linear(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
+                   const void* left, const void* right, int M, int N, float clip_ratio,
+                   const int32_t* weight, int64_t weight_ld, int64_t out_features,
+                   const void* weight_scale, int weight_scale_dtype, const void* bias,
+                   int32_t* codes, float* act_scales,
+                   void* out, int64_t out_ld, void* stream);
+
+/*
  * Dequantize int4 codes: out[t, f] = float(q[t, f]) * float(scales[t]) (float32).
  *
  * Replaces dequantize_int4 (flatquant/ops.py:156-178), which the reference runs

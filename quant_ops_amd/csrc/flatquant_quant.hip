@@ -1120,30 +1120,48 @@ __device__ inline void few_codes_int8(const uint32_t (&yp)[MB][4], float s, int8
   }
 }
 
+// LDS of the few-token routine, carved from one byte array: the X buffers
+// (buffer b of slot p at (b SLOTS + p) XE elements), R's and L's staging rows
+// (one slot; with two, R and then L go through the two slots' second buffers,
+// free at set-up), L's fragments (two slots) and the scale exchange.
+template <int MB, int SLOTS>
+struct FewLds {
+  using S = FewShape<MB>;
+  static constexpr int XE = S::XFRAGS * 512;             // elements of one token's X buffer
+  static constexpr int LF_FRAGS = MB * (S::KS2 + 1);
+  static constexpr int STAGE_E = SLOTS == 1 ? (S::N + S::M) * S::P : 8;
+  static constexpr int XB_OFF = 0;
+  static constexpr int STAGE_OFF = XB_OFF + 2 * SLOTS * XE * 2;
+  static constexpr int LF_OFF = STAGE_OFF + STAGE_E * 2;
+  static constexpr int RED_OFF = LF_OFF + (SLOTS == 1 ? 16 : LF_FRAGS * 1024);
+  static constexpr int BYTES = RED_OFF + SLOTS * 16;
+  static_assert(SLOTS == 1 || (S::N * S::P <= 2 * XE && S::M * S::P <= 2 * XE), "staging fits two X buffers");
+  static_assert(STAGE_OFF % 16 == 0 && LF_OFF % 16 == 0, "16-byte aligned parts");
+};
+
+// The few-token routine of workgroup `group` of `groups`, on the 256 SLOTS
+// threads of the workgroup and LDS of FewLds<MB, SLOTS>::BYTES at `lds`.
 // SLOTS = 1: one token at a time per workgroup, L's fragments in VGPRs (one
 // wave per SIMD). SLOTS = 2 (many tokens): two tokens at a time, four waves
 // each (two waves per SIMD, so one token's MFMA or VALU work can run while the
 // other waits), L's fragments in LDS, shared by all eight waves.
 template <class DT, int MB, bool PACK, int SLOTS>
-__global__ void __launch_bounds__(256 * SLOTS) __attribute__((amdgpu_waves_per_eu(SLOTS, SLOTS)))
-fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
-              const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
-              void* __restrict__ out_codes, float* __restrict__ out_scales) {
+__device__ __attribute__((always_inline)) inline void few_quantize(
+    unsigned char* lds, const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+    const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
+    void* __restrict__ out_codes, float* __restrict__ out_scales, int64_t group, int64_t groups) {
   using S = FewShape<MB>;
+  using LD = FewLds<MB, SLOTS>;
   using T = typename DT::T;
   using V = typename MfmaOps<DT>::V;
+  static_assert(sizeof(T) == 2, "16-bit inputs");
   constexpr int M = S::M, N = S::N, KS1 = S::KS1, KS2 = S::KS2, P = S::P;
-  constexpr int XE = S::XFRAGS * 512;           // elements of one token's X buffer
-  constexpr int LF_FRAGS = MB * (KS2 + 1);
-  // X buffer b of slot p at xb + (b SLOTS + p) XE. With one slot R and L are
-  // staged in arrays of their own; with two, R and then L go through the two
-  // slots' second buffers (free at set-up) and L's fragments get an LDS array.
-  constexpr int STAGE_E = SLOTS == 1 ? (N + M) * P : 8;
-  __shared__ __align__(16) T xb[2 * SLOTS * XE];
-  __shared__ __align__(16) T stage_arr[STAGE_E];
-  __shared__ __align__(16) unsigned char lfs[SLOTS == 1 ? 16 : LF_FRAGS * 1024];
-  __shared__ float red[SLOTS][4];
-  static_assert(SLOTS == 1 || (N * P <= 2 * XE && M * P <= 2 * XE), "staging fits two X buffers");
+  constexpr int XE = LD::XE;
+  constexpr int LF_FRAGS = LD::LF_FRAGS;
+  T* const xb = reinterpret_cast<T*>(lds + LD::XB_OFF);
+  T* const stage_arr = reinterpret_cast<T*>(lds + LD::STAGE_OFF);
+  unsigned char* const lfs = lds + LD::LF_OFF;
+  float* const red = reinterpret_cast<float*>(lds + LD::RED_OFF);
 
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1170,9 +1188,9 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   };
 
   // tokens of slot p: blockIdx SLOTS + p, then every SLOTS grid further on
-  const int64_t stride = (int64_t)gridDim.x * SLOTS;
-  int64_t t = (int64_t)blockIdx.x * SLOTS + p;
-  const int64_t t_slot0 = (int64_t)blockIdx.x * SLOTS;   // slot 0 has at least as many tokens as slot 1
+  const int64_t stride = groups * SLOTS;
+  int64_t t = group * SLOTS + p;
+  const int64_t t_slot0 = group * SLOTS;   // slot 0 has at least as many tokens as slot 1
   T* cur = xb + p * XE;
   T* nxt = xb + (SLOTS + p) * XE;
   issue(t, cur);
@@ -1264,7 +1282,7 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     }
     raw_barrier();
   };
-  float* const red_p = red[p];
+  float* const red_p = red + 4 * p;
   if constexpr (PACK) {
     uint32_t ypp[MB][4];
     float sp, rcpp, amax_d;
@@ -1329,6 +1347,16 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
     }
   }
   wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
+}
+
+template <class DT, int MB, bool PACK, int SLOTS>
+__global__ void __launch_bounds__(256 * SLOTS) __attribute__((amdgpu_waves_per_eu(SLOTS, SLOTS)))
+fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+              const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
+              void* __restrict__ out_codes, float* __restrict__ out_scales) {
+  __shared__ __align__(16) unsigned char lds[FewLds<MB, SLOTS>::BYTES];
+  few_quantize<DT, MB, PACK, SLOTS>(lds, x, tokens, x_ld, left, right, clip, out_codes, out_scales, blockIdx.x,
+                                    gridDim.x);
 }
 
 // ---------------------------------------------------------------------------

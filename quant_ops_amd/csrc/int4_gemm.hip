@@ -22,45 +22,13 @@
 #include <algorithm>
 #include <type_traits>
 
-#include "common.h"
+#include "int4_common.h"
 
 #ifndef QO_GEMM_TILE
 #define QO_GEMM_TILE 256, 256, 128, 4, 2
 #endif
 
 namespace qo {
-
-// Conversions start from a materialised float32 (see opaque()).
-struct OutF16 {
-  using T = _Float16;
-  __device__ static inline T cvt(float v) { return (T)opaque(v); }
-};
-struct OutBF16 {
-  using T = __bf16;
-  __device__ static inline T cvt(float v) { return (T)opaque(v); }
-};
-struct OutF32 {
-  using T = float;
-  __device__ static inline T cvt(float v) { return v; }
-};
-
-// Unpacked signed value of nibble i of a packed word.
-__device__ inline int nib(uint32_t w, int i) { return (int)((w >> (4 * i)) & 0xF) - 8; }
-
-// Epilogue value: (float(acc) * sa) * sb, two separately rounded float32 products.
-__device__ inline float scale_out(int acc, float sa, float sb) {
-  float v = (float)acc * sa;
-  v = v * sb;
-  return v;
-}
-
-// Optional bias in the output type, added to the rounded output as the
-// reference's `output + bias.to(dtype)` does (one float32 add of the two
-// output-type values, one rounding back).
-template <class OT>
-__device__ inline typename OT::T add_bias(typename OT::T v, const typename OT::T* bias, int64_t n) {
-  return bias ? OT::cvt((float)v + (float)bias[n]) : v;
-}
 
 // ---------------------------------------------------------------------------
 // Generic kernel.
@@ -338,39 +306,6 @@ template <int N>
 __device__ inline void gemm_wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt out of range");
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// widen16 in the form gfx950's three-input v_bitop3_b32 takes in one
-// instruction per dword (plus the shift): (w << 4) ^ (0x88888888 << 4) and
-// w ^ 0x88888888, each masked to the high nibbles.
-__device__ inline void widen16_b3(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  lo = ((w << 4) ^ 0x88888880u) & 0xF0F0F0F0u;
-  hi = (w ^ 0x88888888u) & 0xF0F0F0F0u;
-}
-
-// Two packed words -> one 16-byte MFMA operand (low, high dword of each).
-__device__ inline v4i widen_pair(int w0, int w1) {
-  uint32_t l0, h0, l1, h1;
-  widen16_b3((uint32_t)w0, l0, h0);
-  widen16_b3((uint32_t)w1, l1, h1);
-  return v4i{(int)l0, (int)h0, (int)l1, (int)h1};
-}
-
-// Scale element i of a float32 / float16 / bfloat16 vector (dtype fixed at
-// compile time).
-template <int DT>
-__device__ inline float scale_at(const void* p, int64_t i) {
-  if constexpr (DT == QO_DTYPE_F32) return reinterpret_cast<const float*>(p)[i];
-  else if constexpr (DT == QO_DTYPE_F16) return (float)reinterpret_cast<const _Float16*>(p)[i];
-  else return (float)reinterpret_cast<const __bf16*>(p)[i];
-}
-
-// Calls f(std::integral_constant<int, dtype>) for a runtime scale dtype code.
-template <class F>
-__device__ inline void with_scale_dtype(int code, F&& f) {
-  if (code == QO_DTYPE_F32) f(std::integral_constant<int, QO_DTYPE_F32>{});
-  else if (code == QO_DTYPE_F16) f(std::integral_constant<int, QO_DTYPE_F16>{});
-  else f(std::integral_constant<int, QO_DTYPE_BF16>{});
 }
 
 // Which output columns a wave's FN accumulator blocks hold. A block's 16

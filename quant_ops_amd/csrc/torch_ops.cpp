@@ -3,9 +3,11 @@
 //
 // Schemas are those of the reference (flatquant/kernels/cuda_quant_kernel.cu:407-409,
 // int4_matmul/kernels/cuda_int4_matmul_kernel.cu:207-209), so callers of
-// torch.ops.quant_ops.* and graph captures see the same operators. Two
-// operators are additions of this build: int4_matmul_ex (output dtype choice)
-// and dequantize_int4 (a device kernel for the reference's Python function).
+// torch.ops.quant_ops.* and graph captures see the same operators. The others
+// are additions of this build: int4_matmul_ex (output dtype choice),
+// int4_matmul_bias (bias in the epilogue), w4a4_linear (the linear layer's
+// quantize + GEMM as one operator) and dequantize_int4 (a device kernel
+// for the reference's Python function).
 //
 // Unlike the reference, kernels go to the caller's current HIP stream and the
 // host is never synchronised (cuda_quant_kernel.cu:379-385 synchronised the
@@ -139,6 +141,57 @@ at::Tensor int4_matmul_bias(const at::Tensor& a, const at::Tensor& b, const at::
   return int4_matmul_impl(a, b, scale_a, scale_b, out_dtype.value_or(at::kHalf), bias);
 }
 
+// The W4A4 linear layer (w4a4_flatquant_dynamic.py:168-266 on the GPU path):
+// x [T, M*N], weight_packed int32 [out, M*N/8] (the GEMM uses its W.t() view),
+// weight_scale [out] (float32 / float16 / bfloat16), optional bias; output in
+// x's dtype.
+at::Tensor w4a4_linear(const at::Tensor& x, const at::Tensor& left_trans, const at::Tensor& right_trans,
+                       const at::Tensor& weight_packed, const at::Tensor& weight_scale, double clip_ratio,
+                       const std::optional<at::Tensor>& bias) {
+  TORCH_CHECK(x.dim() == 2, "w4a4_linear: x must be 2-D [tokens, features], got ", x.sizes());
+  TORCH_CHECK(left_trans.dim() == 2 && left_trans.size(0) == left_trans.size(1),
+              "w4a4_linear: left_trans must be square [M, M]");
+  TORCH_CHECK(right_trans.dim() == 2 && right_trans.size(0) == right_trans.size(1),
+              "w4a4_linear: right_trans must be square [N, N]");
+  const int64_t T = x.size(0), M = left_trans.size(0), N = right_trans.size(0), F = M * N;
+  TORCH_CHECK(x.size(1) == F, "Input last dimension must equal M*N");
+  TORCH_CHECK(F % 8 == 0, "Features must be divisible by 8 for int32 packing");
+  const int code = dtype_code(x.scalar_type());
+  TORCH_CHECK(code >= 0, "w4a4_linear: x dtype must be float32, float16 or bfloat16, got ", x.scalar_type());
+  TORCH_CHECK(left_trans.scalar_type() == x.scalar_type() && right_trans.scalar_type() == x.scalar_type(),
+              "w4a4_linear: left_trans / right_trans must have x's dtype ", x.scalar_type());
+  TORCH_CHECK(weight_packed.scalar_type() == at::kInt && weight_packed.dim() == 2 && weight_packed.size(1) * 8 == F,
+              "w4a4_linear: weight_packed must be int32 [out_features, M*N/8]");
+  const int64_t NO = weight_packed.size(0);
+  const int swd = dtype_code(weight_scale.scalar_type());
+  TORCH_CHECK(swd >= 0, "w4a4_linear: weight_scale must be float32, float16 or bfloat16");
+  TORCH_CHECK(weight_scale.numel() == NO, "w4a4_linear: weight_scale must hold one value per output channel");
+  TORCH_CHECK(x.is_cuda() && weight_packed.is_cuda() && weight_scale.is_cuda(),
+              "w4a4_linear: x, weight_packed and weight_scale must be GPU tensors");
+  c10::DeviceGuard guard(x.device());
+
+  at::Tensor X = x.stride(1) == 1 && x.stride(0) >= F ? x : x.contiguous();
+  at::Tensor L = left_trans.to(x.device()).contiguous();
+  at::Tensor R = right_trans.to(x.device()).contiguous();
+  at::Tensor W = weight_packed.stride(1) == 1 && weight_packed.stride(0) >= F / 8 ? weight_packed
+                                                                                  : weight_packed.contiguous();
+  at::Tensor sw = weight_scale.reshape({NO}).contiguous();
+  at::Tensor bv;
+  if (bias.has_value()) {
+    TORCH_CHECK(bias->is_cuda() && bias->numel() == NO, "bias must be a GPU tensor of out_features elements");
+    bv = bias->to(x.scalar_type()).reshape({NO}).contiguous();   // the reference adds bias.to(dtype)
+  }
+  at::Tensor codes = at::empty({T, F / 8}, x.options().dtype(at::kInt));
+  at::Tensor scales = at::empty({T}, x.options().dtype(at::kFloat));
+  at::Tensor out = at::empty({T, NO}, x.options());
+  check_status(qo_w4a4_linear(X.data_ptr(), code, T, T > 0 ? X.stride(0) : F, L.data_ptr(), R.data_ptr(), (int)M,
+                              (int)N, (float)clip_ratio, W.data_ptr<int32_t>(), NO > 0 ? W.stride(0) : F / 8, NO,
+                              sw.data_ptr(), swd, bv.defined() ? bv.data_ptr() : nullptr, codes.data_ptr<int32_t>(),
+                              scales.data_ptr<float>(), out.data_ptr(), NO, current_stream(x)),
+               "w4a4_linear");
+  return out;
+}
+
 at::Tensor dequantize_int4(const at::Tensor& quantized, const at::Tensor& scales, bool packed_int32) {
   TORCH_CHECK(quantized.is_cuda() && scales.is_cuda(), "dequantize_int4: tensors must be on the GPU");
   TORCH_CHECK(quantized.dim() == 2, "dequantize_int4: quantized must be 2-D");
@@ -171,6 +224,9 @@ TORCH_LIBRARY(quant_ops, m) {
   m.def(
       "int4_matmul_bias(Tensor a, Tensor b, Tensor scale_a, Tensor scale_b, Tensor bias, "
       "ScalarType? out_dtype=None) -> Tensor");
+  m.def(
+      "w4a4_linear(Tensor x, Tensor left_trans, Tensor right_trans, Tensor weight_packed, Tensor weight_scale, "
+      "float clip_ratio=1, Tensor? bias=None) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(quant_ops, CUDA, m) {
@@ -179,4 +235,5 @@ TORCH_LIBRARY_IMPL(quant_ops, CUDA, m) {
   m.impl("int4_matmul_ex", &int4_matmul_ex);
   m.impl("dequantize_int4", &dequantize_int4);
   m.impl("int4_matmul_bias", &int4_matmul_bias);
+  m.impl("w4a4_linear", &w4a4_linear);
 }

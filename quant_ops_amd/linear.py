@@ -9,8 +9,10 @@ Mirrors the reference's vLLM linear method
 * ``w4a4_flatquant_linear`` is ``apply`` (``:168-266``): per-token dynamic
   quantization of x with the Kronecker transform, the int4 GEMM against the
   packed weight's ``.t()`` view with per-token x per-channel scales, output in
-  x's dtype, then ``+ bias`` (on the GPU fused into the GEMM epilogue with the
-  same two roundings).
+  x's dtype, then ``+ bias``. On the GPU this is one operator
+  (``quant_ops::w4a4_linear``, C ABI ``qo_w4a4_linear``): the two kernels on
+  the current stream, with the bias in the GEMM epilogue (same two
+  roundings).
 
 Differences, each deliberate:
 
@@ -30,6 +32,12 @@ import torch
 from . import _loader
 from .flatquant import flatquant_dynamic_quantize
 from .int4_matmul import int4_matmul, pack_int4_to_int32
+
+
+def _scale_dtype(s: torch.Tensor) -> torch.Tensor:
+    """Weight scales as the operator takes them (float32 / float16 / bfloat16;
+    anything else as float32, which the fallback's float32 product also uses)."""
+    return s if s.dtype in (torch.float32, torch.float16, torch.bfloat16) else s.to(torch.float32)
 
 
 def prepare_w4a4_weight(weight_codes: torch.Tensor) -> torch.Tensor:
@@ -58,15 +66,18 @@ def w4a4_flatquant_linear(
     out_features = weight_packed.shape[0]
     assert weight_packed.shape[1] * 8 == in_features, "weight_packed must be [out, in/8]"
     dtype = x.dtype
-    codes, act_scale = flatquant_dynamic_quantize(
-        x.reshape(-1, in_features), left_trans.to(dtype), right_trans.to(dtype), clip_ratio, pack_int32=True)
-    sa, sb = act_scale.to(torch.float32), weight_scale.reshape(-1).to(torch.float32)
-    if bias is not None and codes.is_cuda:
-        # bias fused into the GEMM epilogue, with the same two roundings
+    x2 = x.reshape(-1, in_features)
+    if x2.is_cuda:
+        # one operator: quantize + GEMM (bias in the GEMM epilogue, with the same
+        # two roundings)
         _loader.require_kernels("w4a4_flatquant_linear")
-        out = torch.ops.quant_ops.int4_matmul_bias(codes, weight_packed.t(), sa, sb, bias.to(dtype), dtype)
-    else:
-        out = int4_matmul(codes, weight_packed.t(), sa, sb, out_dtype=dtype)
-        if bias is not None:
-            out = out + bias.to(dtype)
+        out = torch.ops.quant_ops.w4a4_linear(x2, left_trans.to(dtype), right_trans.to(dtype), weight_packed,
+                                              _scale_dtype(weight_scale.reshape(-1)), float(clip_ratio), bias)
+        return out.view(*x.shape[:-1], out_features)
+    codes, act_scale = flatquant_dynamic_quantize(
+        x2, left_trans.to(dtype), right_trans.to(dtype), clip_ratio, pack_int32=True)
+    sa, sb = act_scale.to(torch.float32), weight_scale.reshape(-1).to(torch.float32)
+    out = int4_matmul(codes, weight_packed.t(), sa, sb, out_dtype=dtype)
+    if bias is not None:
+        out = out + bias.to(dtype)
     return out.view(*x.shape[:-1], out_features)

@@ -27,6 +27,12 @@ if _loader.KERNELS_AVAILABLE:
         def _int4_matmul_bias_fake(a, b, scale_a, scale_b, bias, out_dtype=None):
             return a.new_empty((a.size(0), b.size(1)), dtype=out_dtype or torch.float16)
 
+    if hasattr(torch.ops.quant_ops, "w4a4_linear"):
+
+        @torch.library.register_fake("quant_ops::w4a4_linear")
+        def _w4a4_linear_fake(x, left_trans, right_trans, weight_packed, weight_scale, clip_ratio=1.0, bias=None):
+            return x.new_empty((x.size(0), weight_packed.size(0)), dtype=x.dtype)
+
     @torch.library.register_fake("quant_ops::flatquant_dynamic_quantize")
     def _flatquant_fake(input_tensor, left_trans, right_trans, clip_ratio=1.0, pack_int32=False):
         tokens, feats = input_tensor.shape

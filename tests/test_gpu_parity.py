@@ -785,3 +785,120 @@ def test_w4a4_linear_down_proj(gpu, tokens):
     ref = oi4.int4_matmul_pytorch(q.cpu()[rows], w.t(), s.cpu()[rows], sw, out_dtype=torch.bfloat16)
     assert out.shape == (tokens, 4096) and out.dtype == torch.bfloat16
     assert torch.equal(out.cpu()[rows], ref)
+
+
+# --------------------------------------------------------------------------- the linear layer entry point
+
+def _linear_inputs(tokens, m, n, out_f, dtype, seed, sdt=torch.float32, with_bias=True):
+    x = wl.activations(tokens, m * n, dtype, seed=seed, outlier_frac=0.01, outlier_scale=20.0)
+    L, R = wl.orthogonal(m, seed + 1, dtype), wl.orthogonal(n, seed + 2, dtype)
+    w = wl.random_packed(out_f, m * n // 8, seed + 3)            # [out, in/8]
+    sw = wl.uniform(out_f, 0.001, 0.01, seed + 4).to(sdt)
+    g = torch.Generator().manual_seed(seed + 5)
+    bias = (torch.randn(out_f, generator=g) * 0.5).to(dtype) if with_bias else None
+    return x, L, R, w, sw, bias
+
+
+def _linear_ref(q, s, w, sw, bias, dtype):
+    """The GEMM and bias stage of the fallback, given the kernel's codes and scales."""
+    out = oi4.int4_matmul_pytorch(q.cpu(), w.t(), s.cpu(), sw.float(), out_dtype=dtype)
+    return out + bias.to(dtype) if bias is not None else out
+
+
+LINEAR_CASES = [   # tokens, M, N, out_features, dtype
+    (1, 112, 128, 4096, torch.bfloat16), (16, 112, 128, 4096, torch.bfloat16), (7, 112, 128, 4096, torch.float16),
+    (16, 64, 128, 1024, torch.bfloat16), (3, 96, 128, 2048, torch.float16), (16, 128, 128, 512, torch.bfloat16),
+    (9, 128, 128, 256, torch.float16), (2, 64, 128, 32, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("tokens,m,n,out_f,dtype", LINEAR_CASES)
+@pytest.mark.parametrize("sdt,with_bias,clip", [(torch.float32, True, 0.9), (torch.bfloat16, False, 1.0),
+                                                (torch.float16, True, 1.0)])
+def test_linear_entry_point_matches_kernels_and_oracle(gpu, tokens, m, n, out_f, dtype, sdt, with_bias, clip):
+    """qo_w4a4_linear at decode sizes equals qo_flatquant_quantize followed by
+    qo_int4_gemm(_bias) against W.t() bit for bit (codes, scales, output); the
+    codes and scales meet the quantize bars against the oracle and the output
+    equals the fallback's GEMM + bias on them."""
+    x, L, R, w, sw, bias = _linear_inputs(tokens, m, n, out_f, dtype, 1000 + tokens + m + out_f, sdt, with_bias)
+    _say(f"linear T={tokens} {m}x{n} out={out_f} {dtype} scales {sdt} bias={with_bias} clip={clip}")
+    xd, Ld, Rd, wd, swd = x.to(gpu), L.to(gpu), R.to(gpu), w.to(gpu), sw.to(gpu)
+    bd = bias.to(gpu) if with_bias else None
+    y, q, s = capi.w4a4_linear(xd, Ld, Rd, wd, swd, clip, bd)
+    q2, s2 = capi.flatquant_quantize(xd, Ld, Rd, clip, True)
+    y2 = capi.int4_gemm(q2, wd.t(), s2, swd, out_dtype=dtype, bias=bd)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+    assert y.dtype == dtype and y.shape == (tokens, out_f)
+    assert torch.equal(y, y2)
+    check_quant(x, L, R, clip, True, q, s, f"linear T={tokens} {m}x{n}")
+    assert torch.equal(y.cpu(), _linear_ref(q, s, w, sw, bias, dtype))
+
+
+@pytest.mark.parametrize("tokens,m,n,dtype", [(17, 112, 128, torch.bfloat16), (40, 64, 64, torch.float16),
+                                              (4, 96, 96, torch.bfloat16), (8, 32, 64, torch.float32)])
+def test_linear_entry_point_other_sizes(gpu, tokens, m, n, dtype):
+    """Other shapes and dtypes (more tokens, N != 128, float32 x) through the
+    entry point against the oracle."""
+    out_f = 272
+    x, L, R, w, sw, bias = _linear_inputs(tokens, m, n, out_f, dtype, 77 + tokens)
+    _say(f"linear T={tokens} {m}x{n} {dtype}")
+    y, q, s = capi.w4a4_linear(x.to(gpu), L.to(gpu), R.to(gpu), w.to(gpu), sw.to(gpu), 0.9, bias.to(gpu))
+    torch.cuda.synchronize()
+    check_quant(x, L, R, 0.9, True, q, s, f"linear T={tokens} {m}x{n}")
+    assert torch.equal(y.cpu(), _linear_ref(q, s, w, sw, bias, dtype))
+
+
+def test_linear_graph_replay_and_two_streams(gpu):
+    """The entry point inside a captured HIP graph (replayed several times with
+    eager work in between) and issued on two streams at once: every result
+    equals the eager one."""
+    m, n, out_f, dtype = 112, 128, 4096, torch.bfloat16
+    xs = []
+    for i in range(3):
+        x, L, R, w, sw, bias = _linear_inputs(16, m, n, out_f, dtype, 5150 + i)
+        xs.append(x.to(gpu))
+    Ld, Rd, wd, swd, bd = (t.to(gpu) for t in (L, R, w, sw, bias))
+    eager = [capi.w4a4_linear(x, Ld, Rd, wd, swd, 0.9, bd)[0].clone() for x in xs]
+    outs = [torch.empty_like(e) for e in eager]
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            for x, o in zip(xs, outs):
+                capi.w4a4_linear(x, Ld, Rd, wd, swd, 0.9, bd, out=o)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        capi.w4a4_linear(xs[rep % 3], Ld, Rd, wd, swd, 0.9, bd)    # eager work between replays
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep}"
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    res = []
+    for i in range(6):
+        with torch.cuda.stream(s1 if i % 2 == 0 else s2):
+            res.append((i % 3, capi.w4a4_linear(xs[i % 3], Ld, Rd, wd, swd, 0.9, bd)[0]))
+    torch.cuda.synchronize()
+    for k, y in res:
+        assert torch.equal(y, eager[k])
+
+
+def test_linear_operator_and_module(gpu):
+    """torch.ops.quant_ops.w4a4_linear and w4a4_flatquant_linear (3-D x, [out, 1]
+    scales) give the entry point's output."""
+    m, n, out_f, dtype = 112, 128, 4096, torch.bfloat16
+    x, L, R, w, sw, bias = _linear_inputs(16, m, n, out_f, dtype, 6060, torch.bfloat16)
+    xd, Ld, Rd, wd, swd, bd = (t.to(gpu) for t in (x, L, R, w, sw, bias))
+    y_c = capi.w4a4_linear(xd, Ld, Rd, wd, swd, 0.9, bd)[0]
+    y_op = torch.ops.quant_ops.w4a4_linear(xd, Ld, Rd, wd, swd, 0.9, bd)
+    y_mod = qo.w4a4_flatquant_linear(xd.view(2, 8, -1), Ld, Rd, wd, swd.view(-1, 1), 0.9, bd)
+    torch.cuda.synchronize()
+    assert torch.equal(y_op, y_c) and torch.equal(y_mod.view(16, -1), y_c)
+    with pytest.raises(RuntimeError, match="M\\*N"):
+        torch.ops.quant_ops.w4a4_linear(xd[:, :-8], Ld, Rd, wd, swd, 0.9, bd)
