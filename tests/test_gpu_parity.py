@@ -562,11 +562,14 @@ def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, routing):
     assert torch.equal(out, out_old)
 
 
-# Decode shapes (M <= 64): the skinny kernel, every row-block count, K slices
-# of uneven length over the 8 waves (nk % 8 != 0, nk < 8), ragged N; checked
-# against the oracle and against the tiled kernel on the same inputs.
+# Decode shapes (M <= 64): the skinny kernels, every row-block count, K slices
+# of uneven length over the 8 waves (nk % 8 != 0, nk < 8; for M <= 16 with
+# W.t(): chunk counts below, at and above the 8 waves, a partial last chunk),
+# ragged N; checked against the oracle and against the tiled kernel on the
+# same inputs.
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 14336), (16, 4096, 14336), (7, 100, 128), (32, 36, 640),
-                                   (48, 520, 1152), (64, 64, 4096), (5, 8, 896)])
+                                   (48, 520, 1152), (64, 64, 4096), (5, 8, 896), (3, 300, 2176),
+                                   (16, 40, 15360), (2, 8, 128), (9, 4096, 4096)])
 @pytest.mark.parametrize("bview", [False, True])
 def test_gemm_skinny_bit_exact(gpu, m, n, k, bview, routing):
     case = wl.gemm_case(m, n, k, seed=5 * m + n + k, b_transposed_view=bview)
@@ -583,6 +586,27 @@ def test_gemm_skinny_bit_exact(gpu, m, n, k, bview, routing):
     assert torch.equal(out.cpu(), oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b,
                                                           out_dtype=torch.bfloat16))
     assert torch.equal(out, out_tiled)
+
+
+@pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
+def test_gemm_decode_scale_dtypes_and_bias(gpu, sdt, odt):
+    """The M <= 16 kernel reads its scales as raw bits of any scale dtype and
+    its bias (output dtype) before the main loop: every combination, with and
+    without a bias, bit-exact against the fallback."""
+    m, n, k = 13, 72, 1920
+    case = wl.gemm_case(m, n, k, seed=17, b_transposed_view=True)
+    sa, sb = case.scale_a.to(sdt), case.scale_b.to(sdt)
+    g = torch.Generator().manual_seed(18)
+    bias = (torch.randn(n, generator=g) * 3).to(odt)
+    _say(f"gemm decode {m}x{n}x{k} scales {sdt} out {odt}")
+    args = (case.a.to(gpu), case.b.to(gpu), sa.to(gpu), sb.to(gpu))
+    out = capi.int4_gemm(*args, out_dtype=odt)
+    out_b = capi.int4_gemm(*args, out_dtype=odt, bias=bias.to(gpu))
+    torch.cuda.synchronize()
+    ref = oi4.int4_matmul_pytorch(case.a, case.b, sa, sb, out_dtype=odt)
+    assert torch.equal(out.cpu(), ref)
+    assert torch.equal(out_b.cpu(), ref + bias)
 
 
 @pytest.mark.parametrize("bview", [False, True])
