@@ -74,6 +74,23 @@ __device__ inline float scale_at(const void* p, int64_t i) {
   else return (float)reinterpret_cast<const __bf16*>(p)[i];
 }
 
+// Raw bits of scale element i of a float32 / float16 / bfloat16 vector,
+// loaded without a branch on the dtype: two 16-bit loads at selected
+// addresses (both halves of a float32, or the 16-bit value twice). A kernel
+// can request it before its main loop; nothing waits for it until the
+// epilogue converts it (scale_from_bits).
+__device__ inline uint32_t scale_bits(const void* p, int dtype, int64_t i) {
+  const unsigned short* h = reinterpret_cast<const unsigned short*>(p);
+  const int64_t w = dtype == QO_DTYPE_F32 ? 2 : 1;
+  return (uint32_t)h[w * i] | ((uint32_t)h[w * i + (w - 1)] << 16);
+}
+
+__device__ inline float scale_from_bits(uint32_t bits, int dtype) {
+  return dtype == QO_DTYPE_F32   ? __builtin_bit_cast(float, bits)
+         : dtype == QO_DTYPE_F16 ? (float)__builtin_bit_cast(_Float16, (unsigned short)(bits & 0xFFFFu))
+                                 : __builtin_bit_cast(float, bits << 16);
+}
+
 // Calls f(std::integral_constant<int, dtype>) for a runtime scale dtype code.
 template <class F>
 __device__ inline void with_scale_dtype(int code, F&& f) {

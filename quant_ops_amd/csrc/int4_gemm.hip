@@ -682,6 +682,57 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
   }
 }
 
+// The epilogue of a skinny-kernel lane (row m, columns nc .. nc + 3). Its
+// scales and bias are requested before the main loop (load), as raw bits
+// without a branch on the scale dtype, so that the epilogue (store) does not
+// wait a memory round trip for them: (float(acc) * sa) * sb, one rounding,
+// then add_bias's arithmetic, 8- or 16-byte stores (element stores at the
+// matrix edge).
+template <class OT>
+struct SkinnyEpilogue {
+  using T = typename OT::T;
+  uint32_t sa_bits, sb_bits[4];
+  T bias_v[4] = {};
+
+  __device__ void load(const void* sa, int sad, const void* sb, int sbd, const T* bias, int m, int nc, int M,
+                       int N) {
+    sa_bits = scale_bits(sa, sad, min(m, M - 1));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = min(nc + r, N - 1);
+      sb_bits[r] = scale_bits(sb, sbd, n);
+      if (bias) bias_v[r] = bias[n];
+    }
+  }
+
+  __device__ void store(const v4i& sum, int sad, int sbd, const T* bias, T* out, int64_t ldc, int m, int nc,
+                        int N) const {
+    const float sam = scale_from_bits(sa_bits, sad);
+    T v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const T o = OT::cvt(scale_out(sum[r] >> 8, sam, scale_from_bits(sb_bits[r], sbd)));
+      v[r] = bias ? OT::cvt((float)o + (float)bias_v[r]) : o;
+    }
+    T* o = out + (int64_t)m * ldc + nc;
+    if (nc + 3 < N) {
+      if constexpr (sizeof(T) == 2) {
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        v4s pk;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
+        *reinterpret_cast<v4s*>(o) = pk;
+      } else {
+        *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (nc + r < N) o[r] = v[r];
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // Skinny kernel (gemm_i4_skinny): M <= 64, the decode shapes. The time is the
 // read of B, so the work is spread over columns and K instead of tiles: a
@@ -713,6 +764,9 @@ gemm_i4_skinny(const int32_t* __restrict__ a, int64_t lda, const int32_t* __rest
   const int n0 = blockIdx.x * 16;
   const int nk = K >> 7;
   const int s_begin = wave * nk / 8, s_end = (wave + 1) * nk / 8;
+
+  SkinnyEpilogue<OT> epi;   // waves 0 .. MT-1: row 16 wave + li, columns n0 + 4 lg .. + 3
+  epi.load(sa, sad, sb, sbd, bias, 16 * wave + li, n0 + 4 * lg, M, N);
 
   const int n = min(n0 + li, N - 1);
   const int32_t* bcol = B_NK ? b + (int64_t)n * ldb + 4 * lg : b + (int64_t)(4 * lg) * ldb + n;
@@ -781,29 +835,7 @@ gemm_i4_skinny(const int32_t* __restrict__ a, int64_t lda, const int32_t* __rest
   const int m = 16 * mt + li;
   const int nc = n0 + 4 * lg;
   if (m >= M || nc >= N) return;
-  using T = typename OT::T;
-  const float sam = load_scale(sa, sad, m);
-  T v[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    v[r] = add_bias<OT>(OT::cvt(scale_out(sum[r] >> 8, sam, load_scale(sb, sbd, min(nc + r, N - 1)))), bias,
-                        min(nc + r, N - 1));
-  T* o = out + (int64_t)m * ldc + nc;
-  if (nc + 3 < N) {
-    if constexpr (sizeof(T) == 2) {
-      typedef short v4s __attribute__((ext_vector_type(4)));
-      v4s pk;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
-      *reinterpret_cast<v4s*>(o) = pk;
-    } else {
-      *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (nc + r < N) o[r] = v[r];
-  }
+  epi.store(sum, sad, sbd, bias, out, ldc, m, nc, N);
 }
 
 // ---------------------------------------------------------------------------
@@ -848,6 +880,9 @@ gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __r
   const int nk = K >> 7;                        // stages
   const int rowbytes = K >> 1;                  // bytes of a packed row
   const int nch = (rowbytes + C::CB - 1) / C::CB;
+
+  SkinnyEpilogue<OT> epi;   // waves 0 .. MT-1: row 16 wave + li, columns n0 + 4 lg .. + 3
+  epi.load(sa, sad, sb, sbd, bias, 16 * wave + li, n0 + 4 * lg, M, N);
 
   // DMA instruction t of this wave: SGPR base (its first row), the lane's
   // offset to its row (the second row for CB = 512) and to its swizzled piece,
@@ -930,29 +965,7 @@ gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __r
   const int m = 16 * mt + li;
   const int nc = n0 + 4 * lg;
   if (m >= M || nc >= N) return;
-  using T = typename OT::T;
-  const float sam = load_scale(sa, sad, m);
-  T v[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    v[r] = add_bias<OT>(OT::cvt(scale_out(sum[r] >> 8, sam, load_scale(sb, sbd, min(nc + r, N - 1)))), bias,
-                        min(nc + r, N - 1));
-  T* o = out + (int64_t)m * ldc + nc;
-  if (nc + 3 < N) {
-    if constexpr (sizeof(T) == 2) {
-      typedef short v4s __attribute__((ext_vector_type(4)));
-      v4s pk;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pk[r] = __builtin_bit_cast(short, v[r]);
-      *reinterpret_cast<v4s*>(o) = pk;
-    } else {
-      *reinterpret_cast<v4f*>(o) = v4f{v[0], v[1], v[2], v[3]};
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (nc + r < N) o[r] = v[r];
-  }
+  epi.store(sum, sad, sbd, bias, out, ldc, m, nc, N);
 }
 
 // ---------------------------------------------------------------------------
