@@ -8,8 +8,12 @@
 //
 // Kernels:
 //  * fq_wave_kernel   — one wave per token, M, N <= 64 (fp16 / bf16).
-//  * fq_duo_kernel    — a pair of waves per token, N = 128, M in {64, 96, 112, 128}.
-//  * fq_few_kernel    — the same shapes at up to 128 tokens: four waves per token.
+//  * fq_few_kernel    — N = 128, M in {64, 96, 112, 128}: four waves per token
+//                       (one or two tokens in flight per workgroup).
+//  * fq_few2_kernel   — the same routine in half the registers and LDS, two
+//                       workgroups per CU (112 x 128 and 64 x 128).
+//  * fq_duo_kernel    — a pair of waves per token, the same shapes (kept for
+//                       cross-checks: QO_ROUTE_FQ_NO_FEW routes N = 128 to it).
 //  * fq_mfma_kernel   — D in {fp16, bf16}, the listed shapes: M up to 176 zero-padded
 //                       to 16 MB, N even up to 256 zero-padded to 32 NP.
 //                       Both contractions on v_mfma_f32_16x16x32_{f16,bf16}; X is
@@ -969,7 +973,7 @@ struct FewShape {
 // r + 4 of word 4q + lg of that row; amax = max |Y| of the wave's raw
 // accumulators.
 // lfrag(mb, s) returns L's fragment (mb, s) (from VGPRs or LDS).
-template <class DT, int MB, class LFrag>
+template <class DT, int MB, int G = 4, class LFrag>
 __device__ __attribute__((always_inline)) inline void few_products(
     const typename DT::T* __restrict__ xs, LFrag&& lfrag,
     const typename MfmaOps<DT>::V (&rf)[2][FewShape<MB>::KS1], int lane, uint32_t (&yp)[MB][4], float& amax) {
@@ -980,7 +984,6 @@ __device__ __attribute__((always_inline)) inline void few_products(
   using Epi = FqEpi<DT>;
   constexpr int KS1 = S::KS1, KS2 = S::KS2;
   constexpr int KSL = KS2 + (S::TAIL ? 1 : 0);
-  constexpr int G = 4;
 
   // First product, rounding point 1: zp[h][s][4e + r] = Z[16(2s + e) + 4lg + r][n(h, li)].
   V zp[2][KS2 + 1];
@@ -1357,6 +1360,139 @@ fq_few_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld
   __shared__ __align__(16) unsigned char lds[FewLds<MB, SLOTS>::BYTES];
   few_quantize<DT, MB, PACK, SLOTS>(lds, x, tokens, x_ld, left, right, clip, out_codes, out_scales, blockIdx.x,
                                     gridDim.x);
+}
+
+// ---------------------------------------------------------------------------
+// Compact few-token routine (fq_few2_kernel): the same per-token work as
+// few_quantize with one slot, in at most 256 registers and about 64 KB of LDS,
+// so that two workgroups share a CU (two waves per SIMD: one workgroup's MFMA
+// or VALU work runs while the other waits). Against the one-slot routine:
+// one X buffer (the next token's X is requested once every wave's products
+// have read the current one, i.e. after the scale's barrier, and arrives
+// during the codes); R and then L staged through one area; two row blocks per
+// product step; the codes right after the scale (no cross-token pipelining).
+// ---------------------------------------------------------------------------
+template <int MB>
+struct FewLdsCompact {
+  using S = FewShape<MB>;
+  static constexpr int XE = S::XFRAGS * 512;
+  static constexpr int STAGE_OFF = XE * 2;
+  static constexpr int STAGE_E = (S::N > S::M ? S::N : S::M) * S::P;
+  static constexpr int RED_OFF = STAGE_OFF + STAGE_E * 2;
+  static constexpr int BYTES = RED_OFF + 16;
+  static_assert(STAGE_OFF % 16 == 0 && BYTES <= 80 * 1024, "two workgroups per CU");
+};
+
+template <class DT, int MB, bool PACK>
+__device__ __attribute__((always_inline)) inline void few_quantize_compact(
+    unsigned char* lds, const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+    const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
+    void* __restrict__ out_codes, float* __restrict__ out_scales, int64_t group, int64_t groups) {
+  using S = FewShape<MB>;
+  using LD = FewLdsCompact<MB>;
+  using T = typename DT::T;
+  using V = typename MfmaOps<DT>::V;
+  static_assert(sizeof(T) == 2, "16-bit inputs");
+  constexpr int M = S::M, N = S::N, KS1 = S::KS1, KS2 = S::KS2, P = S::P;
+  T* const xb = reinterpret_cast<T*>(lds);
+  T* const stage = reinterpret_cast<T*>(lds + LD::STAGE_OFF);
+  float* const red = reinterpret_cast<float*>(lds + LD::RED_OFF);
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+  const int q = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's 32-column pair
+
+  // LDS-DMA of token tt's X in fragment order (as few_quantize)
+  auto issue = [&](int64_t tt) {
+    const T* base = x + tt * x_ld + li * N + 8 * lg;
+    const uint32_t lbase = lds_addr(xb);
+#pragma unroll
+    for (int i = 0; i < S::XF_PER_WAVE; ++i) {
+      const int f = q + 4 * i;
+      dma16(base + (f / KS1) * 16 * N + 32 * (f % KS1), lbase + f * 1024);
+    }
+  };
+  int64_t t = group;
+  if (t >= tokens) return;
+  issue(t);
+  // R and L as 16-byte chunks, all loads before any store; R staged first
+  constexpr int RCH = N * N / 8, LCH = M * M / 8;
+  constexpr int RPT = (RCH + 255) / 256, LPT = (LCH + 255) / 256;
+  v4i rtmp[RPT], ltmp[LPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int c = tid + 256 * i;
+    rtmp[i] = reinterpret_cast<const v4i*>(right)[c < RCH ? c : 0];
+  }
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int c = tid + 256 * i;
+    ltmp[i] = reinterpret_cast<const v4i*>(left)[c < LCH ? c : 0];
+  }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int c = tid + 256 * i;   // row c / 16, 8 elements from column 8 (c % 16)
+    if (c < RCH) *reinterpret_cast<v4i*>(stage + (c >> 4) * P + 8 * (c & 15)) = rtmp[i];
+  }
+  lds_barrier();
+  // R's fragments (as few_quantize)
+  V rf[2][KS1];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks) {
+      const T* at = stage + (32 * ks + 8 * lg + (li >> 2)) * P + 32 * q + 8 * (li & 3) + 4 * h;
+      rf[h][ks] = join_tr16<V>(lds_tr16(at), lds_tr16(at + 4 * P));
+    }
+  lds_barrier();   // every wave holds R's fragments: L may overwrite R's rows
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int c = tid + 256 * i;   // row c / (M / 8)
+    if (c < LCH) *reinterpret_cast<v4i*>(stage + (c / (M / 8)) * P + 8 * (c % (M / 8))) = ltmp[i];
+  }
+  lds_barrier();
+  V lf[MB][KS2 + 1];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int sl = 0; sl <= KS2; ++sl) {
+      const T* at = stage + (32 * sl + 4 * lg + (li >> 2)) * P + 16 * mb + 4 * (li & 3);
+      if (sl < KS2) lf[mb][sl] = join_tr16<V>(lds_tr16(at), lds_tr16(at + 16 * P));
+      else if (S::TAIL) lf[mb][sl] = join_tr16<V>(lds_tr16(at), v4s16{0, 0, 0, 0});
+      else lf[mb][sl] = V{};
+    }
+  auto lfrag = [&](int mb, int sl) -> V { return lf[mb][sl]; };
+
+  // One token per iteration: wait for this wave's copies, a barrier for every
+  // wave's (and, from the second token on, for every wave's reads of the
+  // scale exchange), the products, the scale (its barrier ends every wave's
+  // reads of X), the next token's copy, then this token's codes.
+  for (; t < tokens; t += groups) {
+    wait_vmcnt<0>();
+    raw_barrier();
+    uint32_t yp[MB][4];
+    float amax, amax_d;
+    few_products<DT, MB, 2>(xb, lfrag, rf, lane, yp, amax);
+    const float sc = few_scale<DT>(amax, red, q, lane, clip, amax_d);
+    if (t + groups < tokens) issue(t + groups);
+    if (q == 0 && lane == 0) out_scales[t] = sc;
+    if constexpr (PACK) {
+      int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (S::F / 8) + 4 * q + lg;
+      few_codes_packed<DT, MB>(yp, 1.0f / sc, orow, li);
+      if (!(sc > 0.f)) few_codes_zero_scale<DT, MB>(yp, sc, orow, li);
+    } else {
+      few_codes_int8<DT, MB>(yp, sc, reinterpret_cast<int8_t*>(out_codes) + t * S::F + 32 * q + 8 * lg, li);
+    }
+  }
+  wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
+}
+
+template <class DT, int MB, bool PACK>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+fq_few2_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
+               const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
+               void* __restrict__ out_codes, float* __restrict__ out_scales) {
+  __shared__ __align__(16) unsigned char lds[FewLdsCompact<MB>::BYTES];
+  few_quantize_compact<DT, MB, PACK>(lds, x, tokens, x_ld, left, right, clip, out_codes, out_scales, blockIdx.x,
+                                     gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -2046,17 +2182,16 @@ static int launch_wave(const void* x, int64_t tokens, int64_t x_ld, const void* 
   return QO_OK;
 }
 
-// N = 128 shapes take fq_few_kernel at any token count except 64 x 128, where
-// the pair kernel is faster beyond kFewTokensN128 tokens (measured, 8192
-// tokens bf16: 64 x 128 50.1 vs 46.6 us on the pair kernel; 96 x 128 72.4 vs
-// 73.4, 112 x 128 88.3 vs 88.6, fp16 128 x 128 94.7 vs 96.6; 112 x 128 at 256
-// tokens 7.4 vs 10.2, at 4096 tokens 46.4 vs 49.2).
-constexpr int64_t kFewTokensN128 = 128;
-// Tokens per CU above which 96 x 128 keeps two tokens in flight per workgroup
-// (8192 tokens bf16: 72.8 us with two slots vs 75.7 with one). 112 x 128 stays
-// on one slot, which is faster there (8192 tokens 89.3 vs 92.1 us, 4096 tokens
-// 48.9 vs 51.4, 1024 tokens 17.6 vs 20.3); 64 x 128 and 128 x 128 do not fit
-// two slots' buffers beside L's fragments.
+// N = 128 shapes take the few-token routine at every token count. Measured
+// (8192 tokens bf16 unless noted; same process, outputs equal):
+// * 112 x 128 and 64 x 128 run fq_few2_kernel (two workgroups per CU):
+//   112 x 128 82.8-84.4 us against 89.9-90.2 with fq_few_kernel's one slot
+//   (4096 tokens 44.6 vs 48.1, 1024 tokens 16.8 vs 17.3, 16 tokens 6.41 vs
+//   6.46; fp16 88.3 vs 89.0); 64 x 128 44.8 us against 49.3 on the pair
+//   kernel.
+// * 96 x 128 keeps two tokens in flight per workgroup above kFewTwoSlots
+//   tokens per CU (72.8 us with two slots vs 75.7 with one, 73.4 compact).
+// * 128 x 128 stays on one slot (its compact form spills).
 constexpr int64_t kFewTwoSlots = 2;
 
 template <class DT, int MB, bool PACK>
@@ -2073,6 +2208,14 @@ static int launch_few(const void* x, int64_t tokens, int64_t x_ld, const void* l
              reinterpret_cast<const T*>(right), clip, out_codes, out_scales);
       return QO_OK;
     }
+  }
+  if constexpr (MB == 7 || MB == 4) {
+    // one token at a time per workgroup, two workgroups per CU (two waves per SIMD)
+    const int64_t grid = std::min<int64_t>(tokens, 2 * cus);
+    launch((fq_few2_kernel<DT, MB, PACK>), dim3((unsigned)grid), dim3(256), 0, stream, reinterpret_cast<const T*>(x),
+           tokens, x_ld, reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), clip, out_codes,
+           out_scales);
+    return QO_OK;
   }
   // one token at a time per workgroup (four waves, one per SIMD); workgroups loop beyond one per CU
   const int64_t grid = std::min<int64_t>(tokens, cus);
@@ -2140,7 +2283,7 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
 #undef QO_FQ_WAVE_CASE
   }
   // N = 128 at decode token counts: the few-token kernel (scale from max |Y| as well)
-  if (N == 128 && clip > 0.f && clip <= 3.4e38f && fq_route_few() && (tokens <= kFewTokensN128 || M != 64)) {
+  if (N == 128 && clip > 0.f && clip <= 3.4e38f && fq_route_few()) {
 #define QO_FQ_FEW_CASE(MB_)                                                                                  \
     if (M == 16 * (MB_))                                                                                     \
       return launch_few<DT, MB_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream);

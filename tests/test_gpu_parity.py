@@ -264,10 +264,12 @@ def test_quantize_pair_kernel_matches_group_kernel(gpu, tokens, mn, dtype, pack,
 @pytest.mark.parametrize("m", [112, 64, 96, 128])
 @pytest.mark.parametrize("tokens", [1, 16, 37, 128, 600, 1030])
 def test_quantize_few_token_kernel_matches_pair_kernel(gpu, tokens, m, dtype, pack, routing):
-    """N = 128 runs the few-token kernel (four waves per token; 64 x 128 up to
-    128 tokens); it uses the pair kernel's fragment layouts and k order, so
-    codes and scales agree bit for bit (zero token included). 600 and 1030
-    tokens make workgroups loop over several tokens (the pipelined codes)."""
+    """N = 128 runs the few-token routine (four waves per token: fq_few2_kernel
+    with two workgroups per CU for 112 x 128 and 64 x 128, fq_few_kernel with
+    one or two token slots for 96 x 128 and 128 x 128); it uses the pair
+    kernel's fragment layouts and k order, so codes and scales agree bit for
+    bit (zero token included). 600 and 1030 tokens make workgroups loop over
+    several tokens (the refilled X buffer, the pipelined codes)."""
     case = wl.quant_case("few", tokens, m, 128, dtype, 0.9, pack, seed=tokens + 3 * m, outlier_frac=0.005,
                          outlier_scale=30.0)
     case.x[tokens // 2].zero_()
