@@ -73,6 +73,28 @@ def test_c_abi_status_and_errors_without_gpu():
     assert st == 3
     st = lib.qo_dequantize_int4(None, 1, None, 0, 4, 12, None, None)
     assert st == 2
+    # the linear layer's entry point: sizes, strides, dtypes, NULL pointers
+    f = ctypes.c_float(1.0)
+    st = lib.qo_w4a4_linear(None, 2, 4, 14336, None, None, 112, 128, f, None, 1792, 0, None, 0, None, None, None,
+                            None, 4096, None)
+    assert st == 2 and b"out_features" in lib.qo_last_error()
+    st = lib.qo_w4a4_linear(None, 2, 4, 12, None, None, 3, 4, f, None, 2, 16, None, 0, None, None, None, None, 16,
+                            None)
+    assert st == 2 and b"divisible by 8" in lib.qo_last_error()
+    st = lib.qo_w4a4_linear(None, 2, 4, 14336, None, None, 112, 128, f, None, 1000, 4096, None, 0, None, None, None,
+                            None, 4096, None)
+    assert st == 2 and b"row stride" in lib.qo_last_error()
+    st = lib.qo_w4a4_linear(None, 7, 4, 14336, None, None, 112, 128, f, None, 1792, 4096, None, 0, None, None, None,
+                            None, 4096, None)
+    assert st == 3
+    st = lib.qo_w4a4_linear(None, 2, 4, 14336, None, None, 112, 128, f, None, 1792, 4096, None, 9, None, None, None,
+                            None, 4096, None)
+    assert st == 3
+    st = lib.qo_w4a4_linear(None, 2, 4, 14336, None, None, 112, 128, f, None, 1792, 4096, None, 0, None, None, None,
+                            None, 4096, None)
+    assert st == 1
+    assert lib.qo_w4a4_linear(None, 2, 0, 14336, None, None, 112, 128, f, None, 1792, 4096, None, 0, None, None,
+                              None, None, 4096, None) == 0
     # empty problems are valid no-ops
     assert lib.qo_int4_gemm(None, 1, None, 1, 1, None, 0, None, 0, None, 1, 0, 0, 0, 8, None) == 0
     assert lib.qo_flatquant_quantize(None, 1, 0, 64, None, None, 8, 8, ctypes.c_float(1.0), 1, None, None,
@@ -220,6 +242,9 @@ def test_fake_kernels_give_reference_shapes():
         assert o.dtype == torch.bfloat16
         d = torch.ops.quant_ops.dequantize_int4(a, torch.empty(5), True)
         assert d.shape == (5, 32) and d.dtype == torch.float32
+        w = torch.empty(24, 8, dtype=torch.int32)
+        y = torch.ops.quant_ops.w4a4_linear(x, L, L, w, torch.empty(24, dtype=torch.bfloat16), 0.9, None)
+        assert y.shape == (6, 24) and y.dtype == torch.float16
 
 
 def test_workload_generators_are_seeded():
