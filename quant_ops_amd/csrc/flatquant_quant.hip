@@ -80,9 +80,13 @@ __device__ inline int fq_code_from_quot(float t) {
 
 // ---------------------------------------------------------------------------
 // Generic kernel: one 256-thread block per token (grid-stride over tokens).
-// LDS holds X (as D) and Z (as D); Y overwrites X.
+// LDS holds X (as D) and Z (as D); Y overwrites X. With LR_LDS, L and R are
+// copied into LDS once per block as well (where they fit beside X and Z):
+// the products then read every operand from LDS instead of a global load per
+// k step (128 fp32 tokens of 64 x 64: 38.7 -> about 10 us); the arithmetic
+// and its order are the same.
 // ---------------------------------------------------------------------------
-template <class DT, bool PACK>
+template <class DT, bool PACK, bool LR_LDS>
 __global__ void __launch_bounds__(256)
 fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
                   const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right,
@@ -93,10 +97,16 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
   const int F = M * N;
   T* xs = reinterpret_cast<T*>(smem);
   T* zs = xs + F;
+  T* const ls = zs + F;        // LR_LDS: L [M][M], then R [N][N]
+  T* const rs = ls + M * M;
   __shared__ float red_hi[4], red_lo[4], s_scale;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  auto r_at = [&](int i) { return DT::to_f(right[i]); };
-  auto l_at = [&](int i) { return DT::to_f(left[i]); };
+  if constexpr (LR_LDS) {      // ordered before their reads by the token loop's first barrier
+    for (int i = tid; i < M * M; i += 256) ls[i] = left[i];
+    for (int i = tid; i < N * N; i += 256) rs[i] = right[i];
+  }
+  auto r_at = [&](int i) { return DT::to_f(LR_LDS ? rs[i] : right[i]); };
+  auto l_at = [&](int i) { return DT::to_f(LR_LDS ? ls[i] : left[i]); };
 
   for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
     const T* xt = x + t * x_ld;
@@ -2385,7 +2395,7 @@ template <class DT, bool PACK>
 static int launch_generic(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right,
                           int M, int N, float clip, void* out_codes, float* out_scales, hipStream_t stream) {
   using T = typename DT::T;
-  const size_t lds = (size_t)2 * M * N * sizeof(T);
+  size_t lds = (size_t)2 * M * N * sizeof(T);
   constexpr size_t kMaxDynLds = 160 * 1024 - 64;   // the static reduction slots take the rest
   if (lds > kMaxDynLds) {
     // X and Z do not fit together: Y by column blocks, twice per token
@@ -2403,7 +2413,11 @@ static int launch_generic(const void* x, int64_t tokens, int64_t x_ld, const voi
            reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), M, N, clip, out_codes, out_scales);
     return QO_OK;
   }
-  auto kern = fq_generic_kernel<DT, PACK>;
+  // L and R in LDS too where they fit
+  const size_t lds_lr = lds + ((size_t)M * M + (size_t)N * N) * sizeof(T);
+  const bool lr = lds_lr <= kMaxDynLds;
+  auto kern = lr ? fq_generic_kernel<DT, PACK, true> : fq_generic_kernel<DT, PACK, false>;
+  if (lr) lds = lds_lr;
   if (lds > 64 * 1024) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
         hipSuccess) {
