@@ -83,9 +83,37 @@ __device__ inline int fq_code_from_quot(float t) {
 // LDS holds X (as D) and Z (as D); Y overwrites X. With LR_LDS, L and R are
 // copied into LDS once per block as well (where they fit beside X and Z):
 // the products then read every operand from LDS instead of a global load per
-// k step (128 fp32 tokens of 64 x 64: 38.7 -> about 10 us); the arithmetic
-// and its order are the same.
+// k step; the arithmetic and its order are the same.
 // ---------------------------------------------------------------------------
+
+// Four consecutive D elements from LDS as float32 (16- or 8-byte aligned).
+template <class DT>
+__device__ inline v4f lds4(const typename DT::T* p) {
+  using T = typename DT::T;
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const v4f*>(p);
+  } else {
+    typedef T v4t __attribute__((ext_vector_type(4)));
+    const v4t v = *reinterpret_cast<const v4t*>(p);
+    return v4f{DT::to_f(v[0]), DT::to_f(v[1]), DT::to_f(v[2]), DT::to_f(v[3])};
+  }
+}
+
+// n elements from global memory into LDS by 256 threads, eight loads in
+// flight per thread (a plain copy loop waits out each load's latency before
+// the next).
+template <class T>
+__device__ inline void copy_to_lds(T* __restrict__ dst, const T* __restrict__ src, int n, int tid) {
+  int f = tid;
+  for (; f + 7 * 256 < n; f += 8 * 256) {
+    T v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[f + 256 * u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) dst[f + 256 * u] = v[u];
+  }
+  for (; f < n; f += 256) dst[f] = src[f];
+}
 template <class DT, bool PACK, bool LR_LDS>
 __global__ void __launch_bounds__(256)
 fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
@@ -102,24 +130,44 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
   __shared__ float red_hi[4], red_lo[4], s_scale;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if constexpr (LR_LDS) {      // ordered before their reads by the token loop's first barrier
-    for (int i = tid; i < M * M; i += 256) ls[i] = left[i];
-    for (int i = tid; i < N * N; i += 256) rs[i] = right[i];
+    copy_to_lds(ls, left, M * M, tid);
+    copy_to_lds(rs, right, N * N, tid);
   }
   auto r_at = [&](int i) { return DT::to_f(LR_LDS ? rs[i] : right[i]); };
   auto l_at = [&](int i) { return DT::to_f(LR_LDS ? ls[i] : left[i]); };
 
   for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
-    const T* xt = x + t * x_ld;
-    for (int f = tid; f < F; f += 256) xs[f] = xt[f];
+    copy_to_lds(xs, x + t * x_ld, F, tid);
     __syncthreads();
     // Both contractions in 4 x 4 output tiles per thread (rows m0.., columns
     // n0..; consecutive threads take consecutive column groups, so the global
     // reads of R and L coalesce), accumulated in float32 over k in order.
     const int nb = (N + 3) >> 2, tiles = ((M + 3) >> 2) * nb;
+    // With every operand in LDS and M, N multiples of 4, operands are read as
+    // 4-element vectors (rows of X by 4 k, rows of R, L and Z by 4 columns):
+    // two vector reads per k instead of eight scalar ones, same order of
+    // float32 products per output.
+    const bool vec4 = LR_LDS && M % 4 == 0 && N % 4 == 0;
     // Z = rnd_D(X R): Z[m][n] = sum_k X[m][k] R[k][n]
     for (int tl = tid; tl < tiles; tl += 256) {
       const int m0 = tl / nb * 4, n0 = (tl % nb) * 4;
       float acc[4][4] = {};
+      if (vec4) {
+        for (int k = 0; k < N; k += 4) {
+          v4f xv[4], rv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xv[i] = lds4<DT>(xs + (m0 + i) * N + k);
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) rv[kk] = lds4<DT>(rs + (k + kk) * N + n0);
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i][kk], rv[kk][j], acc[i][j]);
+        }
+      } else {
+#pragma unroll 4
       for (int k = 0; k < N; ++k) {
         float xv[4], rv[4];
 #pragma unroll
@@ -130,6 +178,7 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], rv[j], acc[i][j]);
+      }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -143,6 +192,17 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
     for (int tl = tid; tl < tiles; tl += 256) {
       const int m0 = tl / nb * 4, n0 = (tl % nb) * 4;
       float acc[4][4] = {};
+      if (vec4) {
+#pragma unroll 4
+        for (int k = 0; k < M; ++k) {
+          const v4f lv = lds4<DT>(ls + k * M + m0), zv = lds4<DT>(zs + k * N + n0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(lv[i], zv[j], acc[i][j]);
+        }
+      } else {
+#pragma unroll 4
       for (int k = 0; k < M; ++k) {
         float lv[4], zv[4];
 #pragma unroll
@@ -153,6 +213,7 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(lv[i], zv[j], acc[i][j]);
+      }
       }
       // Y goes into X's buffer: X was last read before the barrier above
 #pragma unroll
