@@ -67,7 +67,8 @@ enum qo_route {
   QO_ROUTE_GEMM_GENERIC = 1u << 4,   /* GEMM: every shape on the generic kernel */
   QO_ROUTE_GEMM_NO_DMA = 1u << 5,    /* GEMM: no LDS-DMA tiled kernel */
   QO_ROUTE_GEMM_NO_SKINNY = 1u << 6, /* GEMM: no small-M kernels */
-  QO_ROUTE_ALL = (1u << 7) - 1u
+  QO_ROUTE_LINEAR_NO_READ_AHEAD = 1u << 7, /* linear: no weight read-ahead in the quantize launch */
+  QO_ROUTE_ALL = (1u << 8) - 1u
 };
 unsigned qo_set_kernel_routing(unsigned mask);
 
@@ -151,7 +152,10 @@ int qo_int4_gemm_bias(const int32_t* a, int64_t lda,
  * Kronecker transform (as qo_flatquant_quantize, packed codes), then the int4
  * GEMM against the packed weight with per-token x per-channel scales, output
  * in x's dtype, then + bias (as qo_int4_gemm_bias): those two calls on one
- * stream, so the output equals theirs bit for bit.
+ * stream, so the output equals theirs bit for bit. At up to 64 tokens the
+ * quantize launch also reads the weight ahead with the workgroup slots its
+ * tokens leave idle (reads only; QO_ROUTE_LINEAR_NO_READ_AHEAD switches it
+ * off), so that the GEMM finds the weight in L2.
  *
  * Replaces the GPU path of AscendW4A4FlatQuantDynamicLinearMethod.apply
  * (w4a4_flatquant_dynamic.py:168-266), which runs the quantize operator and

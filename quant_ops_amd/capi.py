@@ -25,7 +25,8 @@ EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_set_kernel_ro
 
 # QO_ROUTE_* bits of qo_set_kernel_routing (include/quant_ops_hip.h)
 ROUTE = {"FQ_GENERIC": 1 << 0, "FQ_NO_WAVE": 1 << 1, "FQ_NO_DUO": 1 << 2, "FQ_NO_FEW": 1 << 3,
-         "GEMM_GENERIC": 1 << 4, "GEMM_NO_DMA": 1 << 5, "GEMM_NO_SKINNY": 1 << 6}
+         "GEMM_GENERIC": 1 << 4, "GEMM_NO_DMA": 1 << 5, "GEMM_NO_SKINNY": 1 << 6,
+         "LINEAR_NO_READ_AHEAD": 1 << 7}
 
 _TORCH_CODE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 

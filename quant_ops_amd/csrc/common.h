@@ -211,6 +211,24 @@ inline void launch(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipS
   }
 }
 
+// A read-ahead request carried by a quantize launch (the linear layer's decode
+// path): the workgroup slots that a few tokens leave idle read the weight rows
+// that the following small-M GEMM streams, each on the XCD whose L2 that
+// GEMM's workgroup will read them through (GEMM workgroup j streams rows
+// 16 j .. 16 j + 15 and runs on XCD j % 8). Results do not depend on it.
+struct ReadAhead {
+  const void* p = nullptr;   // weight rows, 16-byte aligned
+  int64_t rows = 0;
+  int64_t row_bytes = 0;     // row stride in bytes (a multiple of 16)
+  int64_t row_len = 0;       // bytes read from the start of each row (a multiple of 16)
+};
+
+// qo_flatquant_quantize with a read-ahead request (honoured by the kernels
+// that leave CUs idle; ignored by the others). Same arguments and results.
+int flatquant_quantize(const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left, const void* right,
+                       int M, int N, float clip_ratio, int pack_int32, void* out_codes, float* out_scales,
+                       void* stream, const ReadAhead& ahead);
+
 inline int launch_result(const char* who) {
   const hipError_t e = g_launch_error;
   g_launch_error = hipSuccess;

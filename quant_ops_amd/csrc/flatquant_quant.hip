@@ -1577,14 +1577,72 @@ __device__ __attribute__((always_inline)) inline void few_quantize_compact(
   wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
 }
 
+// Read-ahead of workgroup blockIdx (>= qgroups, on XCD blockIdx % 8): the
+// row heads of the GEMM workgroups j with j % 8 == that XCD (rows 16 j ..
+// 16 j + 15, head16 16-byte chunks each, row stride rs16 chunks); the
+// read-ahead workgroups on the XCD take its rows in turn. RB rows at a time,
+// two 16-byte loads per thread and row in flight, values dropped (an empty
+// asm statement takes each): a bounded number of loads in flight, so that the
+// quantize's own loads do not queue behind the whole weight.
+// Read-ahead share of workgroup blockIdx (>= qgroups, on XCD blockIdx % 8):
+// the rows of the GEMM workgroups j with j % 8 == that XCD, listed unit by
+// unit (16 rows, len16 16-byte chunks each; row stride rs16 chunks) and split
+// into equal contiguous shares over the read-ahead workgroups of the XCD.
+// Eight 16-byte loads per thread in flight, the values dropped (an empty asm
+// statement takes each), and a short sleep after each issue: measured at 16
+// tokens (112 x 128 -> 4096 x 14336), the weight read in a burst delays the
+// quantize's own loads (step 17.0 -> 17.2 us), paced at about 320 cycles per
+// load and wave it ends with the quantize (17.0 -> 16.1 us; 1 token 16.2 ->
+// 15.6 us). Reads only; every access is inside the rows given.
+__device__ inline void read_ahead_rows(const v4i* __restrict__ p, int64_t rows, int64_t rs16, int len16,
+                                       int qgroups) {
+  const int b = blockIdx.x, x = b % 8, grid = gridDim.x;
+  const int first = qgroups + ((x - qgroups % 8) + 8) % 8;   // first read-ahead workgroup on this XCD
+  if (first >= grid) return;
+  const int k = (b - first) / 8, nx = (grid - 1 - first) / 8 + 1;
+  const int units = (int)((rows + 15) / 16);
+  const int upx = units > x ? (units - x + 7) / 8 : 0;        // GEMM workgroups on this XCD
+  const int per_unit = 16 * len16, total = upx * per_unit;
+  const int share = (total + nx - 1) / nx, lo = k * share, hi = min(total, lo + share);
+  // element e of the XCD's list: chunk cc of row rr of unit uu (GEMM workgroup x + 8 uu)
+  int e = lo + (int)threadIdx.x;
+  int uu = e / per_unit, rr = e % per_unit / len16, cc = e % len16;
+  while (e < hi) {
+    v4i v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t row = min((int64_t)16 * (x + 8 * uu) + rr, rows - 1);
+      v[u] = p[e < hi ? row * rs16 + cc : 0];
+      __builtin_amdgcn_s_sleep(5);
+      e += 256;   // next element of this thread
+      cc += 256;
+      while (cc >= len16) {
+        cc -= len16;
+        if (++rr == 16) {
+          rr = 0;
+          ++uu;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) asm volatile("" ::"v"(v[u]));
+  }
+}
+
+// Workgroups 0 .. qgroups - 1 quantize; the rest, if any, read ahead.
 template <class DT, int MB, bool PACK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fq_few2_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
                const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
-               void* __restrict__ out_codes, float* __restrict__ out_scales) {
+               void* __restrict__ out_codes, float* __restrict__ out_scales, int qgroups,
+               const v4i* __restrict__ ahead, int64_t ahead_rows, int64_t ahead_rs16, int ahead_len16) {
   __shared__ __align__(16) unsigned char lds[FewLdsCompact<MB>::BYTES];
+  if ((int)blockIdx.x >= qgroups) {
+    read_ahead_rows(ahead, ahead_rows, ahead_rs16, ahead_len16, qgroups);
+    return;
+  }
   few_quantize_compact<DT, MB, PACK>(lds, x, tokens, x_ld, left, right, clip, out_codes, out_scales, blockIdx.x,
-                                     gridDim.x);
+                                     qgroups);
 }
 
 // ---------------------------------------------------------------------------
@@ -2288,7 +2346,7 @@ constexpr int64_t kFewTwoSlots = 2;
 
 template <class DT, int MB, bool PACK>
 static int launch_few(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right, float clip,
-                      void* out_codes, float* out_scales, hipStream_t stream) {
+                      void* out_codes, float* out_scales, hipStream_t stream, const ReadAhead& ra) {
   using T = typename DT::T;
   const int64_t cus = device_cu_count();
   if constexpr (MB == 6) {
@@ -2302,11 +2360,17 @@ static int launch_few(const void* x, int64_t tokens, int64_t x_ld, const void* l
     }
   }
   if constexpr (MB == 7 || MB == 4) {
-    // one token at a time per workgroup, two workgroups per CU (two waves per SIMD)
+    // one token at a time per workgroup, two workgroups per CU (two waves per SIMD);
+    // a read-ahead request takes the workgroup slots the tokens leave free
     const int64_t grid = std::min<int64_t>(tokens, 2 * cus);
-    launch((fq_few2_kernel<DT, MB, PACK>), dim3((unsigned)grid), dim3(256), 0, stream, reinterpret_cast<const T*>(x),
-           tokens, x_ld, reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), clip, out_codes,
-           out_scales);
+    const bool ahead = ra.p && ra.rows > 0 && ra.row_len >= 16 && (uintptr_t)ra.p % 16 == 0 &&
+                       ra.row_bytes % 16 == 0 && ra.row_len % 16 == 0 && ra.row_len <= ra.row_bytes &&
+                       (ra.rows + 256) * (ra.row_len / 16) < INT32_MAX / 2 && grid < 2 * cus;
+    launch((fq_few2_kernel<DT, MB, PACK>), dim3((unsigned)(ahead ? 2 * cus : grid)), dim3(256), 0, stream,
+           reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
+           reinterpret_cast<const T*>(right), clip, out_codes, out_scales, (int)grid,
+           reinterpret_cast<const v4i*>(ra.p), ahead ? ra.rows : (int64_t)0, ra.row_bytes / 16,
+           ahead ? (int)(ra.row_len / 16) : 0);
     return QO_OK;
   }
   // one token at a time per workgroup (four waves, one per SIMD); workgroups loop beyond one per CU
@@ -2353,7 +2417,7 @@ static bool fq_route_few() {
 template <class DT, bool PACK>
 static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_ld, const void* left,
                          const void* right, float clip, void* out_codes, float* out_scales,
-                         hipStream_t stream, bool* handled) {
+                         hipStream_t stream, bool* handled, const ReadAhead& ra) {
   *handled = true;
   // Up to a few hundred tokens the workgroup kernel (fq_mfma_kernel, one
   // token per group of 2-4 waves) finishes sooner than the one-wave and pair
@@ -2378,7 +2442,7 @@ static int dispatch_mfma(int M, int N, const void* x, int64_t tokens, int64_t x_
   if (N == 128 && clip > 0.f && clip <= 3.4e38f && fq_route_few()) {
 #define QO_FQ_FEW_CASE(MB_)                                                                                  \
     if (M == 16 * (MB_))                                                                                     \
-      return launch_few<DT, MB_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream);
+      return launch_few<DT, MB_, PACK>(x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream, ra);
     QO_FQ_FEW_CASE(7)   // 112 x 128 (hidden 14336)
     QO_FQ_FEW_CASE(4)   // 64 x 128  (hidden 8192)
     QO_FQ_FEW_CASE(8)   // 128 x 128 (hidden 16384)
@@ -2497,7 +2561,7 @@ static int launch_generic(const void* x, int64_t tokens, int64_t x_ld, const voi
 template <class DT, bool PACK>
 static int run_quantize(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right, int M,
                         int N, float clip, void* out_codes, float* out_scales, hipStream_t stream,
-                        bool allow_mfma) {
+                        bool allow_mfma, const ReadAhead& ra) {
   if constexpr (DT::code != QO_DTYPE_F32) {
     // 16-byte vector loads of X rows and of L / R rows, vector stores of codes
     const bool aligned = ((uintptr_t)x % 16 == 0) && ((x_ld * (int64_t)sizeof(typename DT::T)) % 16 == 0) &&
@@ -2506,7 +2570,7 @@ static int run_quantize(const void* x, int64_t tokens, int64_t x_ld, const void*
     if (allow_mfma && aligned) {
       bool handled = false;
       int st = dispatch_mfma<DT, PACK>(M, N, x, tokens, x_ld, left, right, clip, out_codes, out_scales, stream,
-                                       &handled);
+                                       &handled, ra);
       if (handled) return st;
     }
   }
@@ -2521,9 +2585,9 @@ static bool fq_allow_mfma() {
   return !qo::route_off(QO_ROUTE_FQ_GENERIC);
 }
 
-extern "C" int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
-                                     const void* right, int M, int N, float clip_ratio, int pack_int32,
-                                     void* out_codes, float* out_scales, void* stream) {
+int qo::flatquant_quantize(const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
+                           const void* right, int M, int N, float clip_ratio, int pack_int32, void* out_codes,
+                           float* out_scales, void* stream, const ReadAhead& ra) {
   using namespace qo;
   if (tokens < 0 || M < 1 || N < 1) {
     qo_set_error("qo_flatquant_quantize: invalid sizes tokens=%lld M=%d N=%d", (long long)tokens, M, N);
@@ -2550,21 +2614,21 @@ extern "C" int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens,
   switch (x_dtype) {
     case QO_DTYPE_F32:
       st = pack_int32 ? run_quantize<F32T, true>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
-                                                  out_scales, s, mf)
+                                                  out_scales, s, mf, ra)
                       : run_quantize<F32T, false>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
-                                                   out_scales, s, mf);
+                                                   out_scales, s, mf, ra);
       break;
     case QO_DTYPE_F16:
       st = pack_int32 ? run_quantize<F16T, true>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
-                                                  out_scales, s, mf)
+                                                  out_scales, s, mf, ra)
                       : run_quantize<F16T, false>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
-                                                   out_scales, s, mf);
+                                                   out_scales, s, mf, ra);
       break;
     case QO_DTYPE_BF16:
       st = pack_int32 ? run_quantize<BF16T, true>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
-                                                   out_scales, s, mf)
+                                                   out_scales, s, mf, ra)
                       : run_quantize<BF16T, false>(x, tokens, x_ld, left, right, M, N, clip_ratio, out_codes,
-                                                    out_scales, s, mf);
+                                                    out_scales, s, mf, ra);
       break;
     default:
       qo_set_error("qo_flatquant_quantize: unsupported input dtype code %d", x_dtype);
@@ -2572,4 +2636,11 @@ extern "C" int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens,
   }
   const int lst = launch_result("qo_flatquant_quantize");
   return st != QO_OK ? st : lst;
+}
+
+extern "C" int qo_flatquant_quantize(const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
+                                     const void* right, int M, int N, float clip_ratio, int pack_int32,
+                                     void* out_codes, float* out_scales, void* stream) {
+  return qo::flatquant_quantize(x, x_dtype, tokens, x_ld, left, right, M, N, clip_ratio, pack_int32, out_codes,
+                                out_scales, stream, qo::ReadAhead{});
 }

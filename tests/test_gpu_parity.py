@@ -860,6 +860,27 @@ def test_linear_entry_point_matches_kernels_and_oracle(gpu, tokens, m, n, out_f,
     assert torch.equal(y.cpu(), _linear_ref(q, s, w, sw, bias, dtype))
 
 
+@pytest.mark.parametrize("tokens,m,out_f,pad", [(1, 112, 4100, 4), (5, 112, 4096, 0), (16, 112, 4100, 4),
+                                               (16, 64, 1000, 8), (3, 64, 16, 0)])
+def test_linear_read_ahead_changes_nothing(gpu, tokens, m, out_f, pad):
+    """At decode token counts the linear call's quantize launch also reads the
+    weight ahead; with that switched off (QO_ROUTE_LINEAR_NO_READ_AHEAD) every
+    output is the same, bit for bit, including a weight with padded rows (row
+    stride above the row length) and out_features not a multiple of 16."""
+    x, L, R, w, sw, bias = _linear_inputs(tokens, m, 128, out_f, torch.bfloat16, 4321 + tokens + out_f)
+    wide = torch.zeros(out_f, w.shape[1] + pad, dtype=torch.int32)
+    wide[:, :w.shape[1]] = w
+    _say(f"linear read-ahead T={tokens} {m}x128 out={out_f} pad={pad}")
+    xd, Ld, Rd, swd, bd = x.to(gpu), L.to(gpu), R.to(gpu), sw.to(gpu), bias.to(gpu)
+    wd = wide.to(gpu)[:, :w.shape[1]]
+    y, q, s = capi.w4a4_linear(xd, Ld, Rd, wd, swd, 0.9, bd)
+    with capi.kernel_routing("LINEAR_NO_READ_AHEAD"):
+        y0, q0, s0 = capi.w4a4_linear(xd, Ld, Rd, wd, swd, 0.9, bd)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q0) and torch.equal(s, s0) and torch.equal(y, y0)
+    assert torch.equal(y.cpu(), _linear_ref(q, s, w, sw, bias, torch.bfloat16))
+
+
 @pytest.mark.parametrize("tokens,m,n,dtype", [(17, 112, 128, torch.bfloat16), (40, 64, 64, torch.float16),
                                               (4, 96, 96, torch.bfloat16), (8, 32, 64, torch.float32)])
 def test_linear_entry_point_other_sizes(gpu, tokens, m, n, dtype):
