@@ -79,109 +79,111 @@ __device__ inline int fq_code_from_quot(float t) {
 }
 
 // ---------------------------------------------------------------------------
-// Generic kernel: one 256-thread block per token (grid-stride over tokens).
+// Generic kernel: one block of BT threads per token (grid-stride over tokens).
 // LDS holds X (as D) and Z (as D); Y overwrites X. With LR_LDS, L and R are
 // copied into LDS once per block as well (where they fit beside X and Z):
 // the products then read every operand from LDS instead of a global load per
-// k step; the arithmetic and its order are the same.
+// k step; the arithmetic and its order are the same. Each thread accumulates
+// TM x 4 output tiles (TM = 4 with 256 threads; TM = 2 with 512 threads, for
+// fewer tokens than CUs: two waves per SIMD, half the products per wave).
 // ---------------------------------------------------------------------------
 
-// Four consecutive D elements from LDS as float32 (16- or 8-byte aligned).
-template <class DT>
-__device__ inline v4f lds4(const typename DT::T* p) {
+// W consecutive D elements from LDS as float32 (W = 2 or 4; 4 W- or
+// 2 W-byte aligned).
+template <class DT, int W>
+__device__ inline void ldsv(const typename DT::T* p, float (&out)[W]) {
   using T = typename DT::T;
-  if constexpr (sizeof(T) == 4) {
-    return *reinterpret_cast<const v4f*>(p);
-  } else {
-    typedef T v4t __attribute__((ext_vector_type(4)));
-    const v4t v = *reinterpret_cast<const v4t*>(p);
-    return v4f{DT::to_f(v[0]), DT::to_f(v[1]), DT::to_f(v[2]), DT::to_f(v[3])};
-  }
+  typedef T vt __attribute__((ext_vector_type(W)));
+  const vt v = *reinterpret_cast<const vt*>(p);
+#pragma unroll
+  for (int i = 0; i < W; ++i) out[i] = DT::to_f(v[i]);
 }
 
-// n elements from global memory into LDS by 256 threads, eight loads in
-// flight per thread (a plain copy loop waits out each load's latency before
-// the next).
-template <class T>
+// n elements from global memory into LDS by BT threads, eight loads in flight
+// per thread (a plain copy loop waits out each load's latency before the
+// next).
+template <int BT, class T>
 __device__ inline void copy_to_lds(T* __restrict__ dst, const T* __restrict__ src, int n, int tid) {
   int f = tid;
-  for (; f + 7 * 256 < n; f += 8 * 256) {
+  for (; f + 7 * BT < n; f += 8 * BT) {
     T v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src[f + 256 * u];
+    for (int u = 0; u < 8; ++u) v[u] = src[f + BT * u];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) dst[f + 256 * u] = v[u];
+    for (int u = 0; u < 8; ++u) dst[f + BT * u] = v[u];
   }
-  for (; f < n; f += 256) dst[f] = src[f];
+  for (; f < n; f += BT) dst[f] = src[f];
 }
-template <class DT, bool PACK, bool LR_LDS>
-__global__ void __launch_bounds__(256)
+
+template <class DT, bool PACK, bool LR_LDS, int BT, int TM>
+__global__ void __launch_bounds__(BT)
 fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
                   const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right,
                   int M, int N, float clip, void* __restrict__ out_codes,
                   float* __restrict__ out_scales) {
+  static_assert(BT % 64 == 0 && (TM == 2 || TM == 4), "block and tile");
   using T = typename DT::T;
+  constexpr int NWV = BT / 64;
   extern __shared__ __align__(16) unsigned char smem[];
   const int F = M * N;
   T* xs = reinterpret_cast<T*>(smem);
   T* zs = xs + F;
   T* const ls = zs + F;        // LR_LDS: L [M][M], then R [N][N]
   T* const rs = ls + M * M;
-  __shared__ float red_hi[4], red_lo[4], s_scale;
+  __shared__ float red_hi[NWV], red_lo[NWV], s_scale;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if constexpr (LR_LDS) {      // ordered before their reads by the token loop's first barrier
-    copy_to_lds(ls, left, M * M, tid);
-    copy_to_lds(rs, right, N * N, tid);
+    copy_to_lds<BT>(ls, left, M * M, tid);
+    copy_to_lds<BT>(rs, right, N * N, tid);
   }
   auto r_at = [&](int i) { return DT::to_f(LR_LDS ? rs[i] : right[i]); };
   auto l_at = [&](int i) { return DT::to_f(LR_LDS ? ls[i] : left[i]); };
 
   for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
-    copy_to_lds(xs, x + t * x_ld, F, tid);
+    copy_to_lds<BT>(xs, x + t * x_ld, F, tid);
     __syncthreads();
-    // Both contractions in 4 x 4 output tiles per thread (rows m0.., columns
+    // Both contractions in TM x 4 output tiles per thread (rows m0.., columns
     // n0..; consecutive threads take consecutive column groups, so the global
     // reads of R and L coalesce), accumulated in float32 over k in order.
-    const int nb = (N + 3) >> 2, tiles = ((M + 3) >> 2) * nb;
+    const int nb = (N + 3) >> 2, tiles = ((M + TM - 1) / TM) * nb;
     // With every operand in LDS and M, N multiples of 4, operands are read as
-    // 4-element vectors (rows of X by 4 k, rows of R, L and Z by 4 columns):
-    // two vector reads per k instead of eight scalar ones, same order of
-    // float32 products per output.
-    const bool vec4 = LR_LDS && M % 4 == 0 && N % 4 == 0;
+    // vectors (rows of X by 4 k, rows of R and Z by 4 columns, L by TM
+    // columns): same order of float32 products per output.
+    const bool vec = LR_LDS && M % 4 == 0 && N % 4 == 0;
     // Z = rnd_D(X R): Z[m][n] = sum_k X[m][k] R[k][n]
-    for (int tl = tid; tl < tiles; tl += 256) {
-      const int m0 = tl / nb * 4, n0 = (tl % nb) * 4;
-      float acc[4][4] = {};
-      if (vec4) {
+    for (int tl = tid; tl < tiles; tl += BT) {
+      const int m0 = tl / nb * TM, n0 = (tl % nb) * 4;
+      float acc[TM][4] = {};
+      if (vec) {
         for (int k = 0; k < N; k += 4) {
-          v4f xv[4], rv[4];
+          float xv[TM][4], rv[4][4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) xv[i] = lds4<DT>(xs + (m0 + i) * N + k);
+          for (int i = 0; i < TM; ++i) ldsv<DT, 4>(xs + (m0 + i) * N + k, xv[i]);
 #pragma unroll
-          for (int kk = 0; kk < 4; ++kk) rv[kk] = lds4<DT>(rs + (k + kk) * N + n0);
+          for (int kk = 0; kk < 4; ++kk) ldsv<DT, 4>(rs + (k + kk) * N + n0, rv[kk]);
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
               for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i][kk], rv[kk][j], acc[i][j]);
         }
       } else {
 #pragma unroll 4
-      for (int k = 0; k < N; ++k) {
-        float xv[4], rv[4];
+        for (int k = 0; k < N; ++k) {
+          float xv[TM], rv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xv[i] = m0 + i < M ? DT::to_f(xs[(m0 + i) * N + k]) : 0.f;
+          for (int i = 0; i < TM; ++i) xv[i] = m0 + i < M ? DT::to_f(xs[(m0 + i) * N + k]) : 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) rv[j] = n0 + j < N ? r_at(k * N + n0 + j) : 0.f;
+          for (int j = 0; j < 4; ++j) rv[j] = n0 + j < N ? r_at(k * N + n0 + j) : 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], rv[j], acc[i][j]);
+            for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], rv[j], acc[i][j]);
+        }
       }
-      }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if (m0 + i < M && n0 + j < N) zs[(m0 + i) * N + n0 + j] = DT::from_f(acc[i][j]);
@@ -189,35 +191,37 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
     __syncthreads();
     // Y = rnd_D(L^T Z): Y[m][n] = sum_k L[k][m] Z[k][n]
     float hi = -INFINITY, lo = INFINITY;
-    for (int tl = tid; tl < tiles; tl += 256) {
-      const int m0 = tl / nb * 4, n0 = (tl % nb) * 4;
-      float acc[4][4] = {};
-      if (vec4) {
+    for (int tl = tid; tl < tiles; tl += BT) {
+      const int m0 = tl / nb * TM, n0 = (tl % nb) * 4;
+      float acc[TM][4] = {};
+      if (vec) {
 #pragma unroll 4
         for (int k = 0; k < M; ++k) {
-          const v4f lv = lds4<DT>(ls + k * M + m0), zv = lds4<DT>(zs + k * N + n0);
+          float lv[TM], zv[4];
+          ldsv<DT, TM>(ls + k * M + m0, lv);
+          ldsv<DT, 4>(zs + k * N + n0, zv);
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(lv[i], zv[j], acc[i][j]);
         }
       } else {
 #pragma unroll 4
-      for (int k = 0; k < M; ++k) {
-        float lv[4], zv[4];
+        for (int k = 0; k < M; ++k) {
+          float lv[TM], zv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) lv[i] = m0 + i < M ? l_at(k * M + m0 + i) : 0.f;
+          for (int i = 0; i < TM; ++i) lv[i] = m0 + i < M ? l_at(k * M + m0 + i) : 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) zv[j] = n0 + j < N ? DT::to_f(zs[k * N + n0 + j]) : 0.f;
+          for (int j = 0; j < 4; ++j) zv[j] = n0 + j < N ? DT::to_f(zs[k * N + n0 + j]) : 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(lv[i], zv[j], acc[i][j]);
-      }
+            for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(lv[i], zv[j], acc[i][j]);
+        }
       }
       // Y goes into X's buffer: X was last read before the barrier above
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if (m0 + i < M && n0 + j < N) {
@@ -233,7 +237,7 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
     __syncthreads();
     if (tid == 0) {
       float h = red_hi[0], l = red_lo[0];
-      for (int w = 1; w < 4; ++w) { h = fmaxf(h, red_hi[w]); l = fminf(l, red_lo[w]); }
+      for (int w = 1; w < NWV; ++w) { h = fmaxf(h, red_hi[w]); l = fminf(l, red_lo[w]); }
       const float s = fq_scale<DT>(h, l, clip);
       s_scale = s;
       out_scales[t] = s;
@@ -242,7 +246,7 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
     const float s = s_scale;
     if (PACK) {
       int32_t* o = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8);
-      for (int p = tid; p < F / 8; p += 256) {
+      for (int p = tid; p < F / 8; p += BT) {
         uint32_t word = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -253,7 +257,7 @@ fq_generic_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t 
       }
     } else {
       int8_t* o = reinterpret_cast<int8_t*>(out_codes) + t * F;
-      for (int f = tid; f < F; f += 256) {
+      for (int f = tid; f < F; f += BT) {
         const float q = DT::round(opaque(DT::to_f(xs[f])) / s);
         o[f] = (int8_t)fq_code_from_quot<false>(q);
       }
@@ -2538,10 +2542,14 @@ static int launch_generic(const void* x, int64_t tokens, int64_t x_ld, const voi
            reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), M, N, clip, out_codes, out_scales);
     return QO_OK;
   }
-  // L and R in LDS too where they fit
+  // L and R in LDS too where they fit; fewer tokens than CUs: 512 threads per
+  // token (two waves per SIMD, half the products each)
   const size_t lds_lr = lds + ((size_t)M * M + (size_t)N * N) * sizeof(T);
   const bool lr = lds_lr <= kMaxDynLds;
-  auto kern = lr ? fq_generic_kernel<DT, PACK, true> : fq_generic_kernel<DT, PACK, false>;
+  const int cus = device_cu_count();
+  const bool wide = tokens < cus;
+  auto kern = wide ? (lr ? fq_generic_kernel<DT, PACK, true, 512, 2> : fq_generic_kernel<DT, PACK, false, 512, 2>)
+                   : (lr ? fq_generic_kernel<DT, PACK, true, 256, 4> : fq_generic_kernel<DT, PACK, false, 256, 4>);
   if (lr) lds = lds_lr;
   if (lds > 64 * 1024) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
@@ -2550,9 +2558,9 @@ static int launch_generic(const void* x, int64_t tokens, int64_t x_ld, const voi
       return QO_ERR_UNSUPPORTED;
     }
   }
-  int64_t grid = (int64_t)device_cu_count() * 4;
+  int64_t grid = (int64_t)cus * 4;
   if (grid > tokens) grid = tokens;
-  launch(kern, dim3((unsigned)grid), dim3(256), lds, stream, reinterpret_cast<const T*>(x), tokens,
+  launch(kern, dim3((unsigned)grid), dim3(wide ? 512 : 256), lds, stream, reinterpret_cast<const T*>(x), tokens,
                      x_ld, reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), M, N, clip,
                      out_codes, out_scales);
   return QO_OK;
