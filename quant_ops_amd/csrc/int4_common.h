@@ -65,6 +65,19 @@ __device__ inline v4i widen_pair(int w0, int w1) {
   return v4i{(int)l0, (int)h0, (int)l1, (int)h1};
 }
 
+// widen_pair of words 2h and 2h + 1 of a 16-byte register group: both words'
+// shifts by one v_lshlrev_b64 (the bits crossing between the two words land
+// in nibbles the mask drops; as C the compiler splits it into two 32-bit
+// shifts). Same values as widen_pair.
+__device__ inline v4i widen_pair64(const v4i& w, int h) {
+  typedef unsigned long long u64;
+  const uint32_t w0 = (uint32_t)w[2 * h], w1 = (uint32_t)w[2 * h + 1];
+  u64 sh;
+  asm("v_lshlrev_b64 %0, 4, %1" : "=v"(sh) : "v"(((u64)w1 << 32) | w0));
+  return v4i{(int)(((uint32_t)sh ^ 0x88888880u) & 0xF0F0F0F0u), (int)((w0 ^ 0x88888888u) & 0xF0F0F0F0u),
+             (int)(((uint32_t)(sh >> 32) ^ 0x88888880u) & 0xF0F0F0F0u), (int)((w1 ^ 0x88888888u) & 0xF0F0F0F0u)};
+}
+
 // Scale element i of a float32 / float16 / bfloat16 vector (dtype fixed at
 // compile time).
 template <int DT>

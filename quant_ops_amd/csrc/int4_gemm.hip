@@ -607,10 +607,12 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
     for (int h = 0; h < 2; ++h) {
       v4i fa[FM];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) fa[i] = widen_pair(ar[P][i][2 * h], ar[P][i][2 * h + 1]);
+      for (int i = 0; i < FM; ++i) fa[i] = widen_pair64(ar[P][i], h);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const v4i fb = widen_pair(word(set, j, 2 * h), word(set, j, 2 * h + 1));
+        v4i fb;
+        if constexpr (B_NK) fb = widen_pair64(br[P][j], h);
+        else fb = widen_pair(word(set, j, 2 * h), word(set, j, 2 * h + 1));
 #pragma unroll
         for (int i = 0; i < FM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, fa[i], acc[i][j], 0, 0, 0);
       }
@@ -803,11 +805,11 @@ gemm_i4_skinny(const int32_t* __restrict__ a, int64_t lda, const int32_t* __rest
       if (s0 + c >= s_end) break;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const v4i fb = widen_pair(bq[P][c][2 * h], bq[P][c][2 * h + 1]);
+        const v4i fb = widen_pair64(bq[P][c], h);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-              fb, widen_pair(aq[P][c][mt][2 * h], aq[P][c][mt][2 * h + 1]), acc[mt], 0, 0, 0);
+              fb, widen_pair64(aq[P][c][mt], h), acc[mt], 0, 0, 0);
       }
     }
   };
@@ -932,10 +934,10 @@ gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __r
         aw[mt] = *reinterpret_cast<const v4i*>(base + (16 + 16 * mt + li) * C::CB + 16 * slot);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const v4i fb = widen_pair(bw[2 * h], bw[2 * h + 1]);
+        const v4i fb = widen_pair64(bw, h);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, widen_pair(aw[mt][2 * h], aw[mt][2 * h + 1]), acc[mt],
+          acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, widen_pair64(aw[mt], h), acc[mt],
                                                           0, 0, 0);
       }
     }
