@@ -1553,9 +1553,13 @@ __device__ __attribute__((always_inline)) inline void few_quantize_compact(
   // One token per iteration: wait for this wave's copies, a barrier for every
   // wave's (and, from the second token on, for every wave's reads of the
   // scale exchange), the products, the scale, then this token's codes; the
-  // next token's copy goes out once every wave's reads of X are done.
+  // next token's copy goes out once every wave's reads of X are done. Vector
+  // memory operations retire in order, and after a token's copies every wave
+  // issues at least MB code stores of the token before: waiting until at
+  // most MB remain waits for the copies, not for those stores.
   for (; t < tokens; t += groups) {
-    wait_vmcnt<0>();
+    if (t == group) wait_vmcnt<0>();
+    else wait_vmcnt<MB>();
     raw_barrier();
     uint32_t yp[MB][4];
     float amax, amax_d;
