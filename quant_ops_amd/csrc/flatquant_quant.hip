@@ -1585,13 +1585,6 @@ __device__ __attribute__((always_inline)) inline void few_quantize_compact(
   wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
 }
 
-// Read-ahead of workgroup blockIdx (>= qgroups, on XCD blockIdx % 8): the
-// row heads of the GEMM workgroups j with j % 8 == that XCD (rows 16 j ..
-// 16 j + 15, head16 16-byte chunks each, row stride rs16 chunks); the
-// read-ahead workgroups on the XCD take its rows in turn. RB rows at a time,
-// two 16-byte loads per thread and row in flight, values dropped (an empty
-// asm statement takes each): a bounded number of loads in flight, so that the
-// quantize's own loads do not queue behind the whole weight.
 // Read-ahead share of workgroup blockIdx (>= qgroups, on XCD blockIdx % 8):
 // the rows of the GEMM workgroups j with j % 8 == that XCD, listed unit by
 // unit (16 rows, len16 16-byte chunks each; row stride rs16 chunks) and split
