@@ -1357,12 +1357,17 @@ __device__ __attribute__((always_inline)) inline void few_quantize(
   //
   // Packed codes are software-pipelined: token i's codes (VALU work) are
   // computed in the iteration of token i + 1's products (MFMA work).
-  auto next_x = [&](int64_t tn) {
+  // stored: this wave issued a token's MB code stores after the current
+  // buffer's copies (the pipelined packed loop below): then those stores may
+  // stay outstanding too, since copies and stores retire in order.
+  auto next_x = [&](int64_t tn, bool stored = false) {
     if (tn < tokens + (SLOTS - 1)) {   // slot 1 copies (a valid row) as long as slot 0 has a token
       issue(tn, nxt);
-      wait_vmcnt<S::XF_PER_WAVE>();
+      if (stored) wait_vmcnt<S::XF_PER_WAVE + MB>();
+      else wait_vmcnt<S::XF_PER_WAVE>();
     } else {
-      wait_vmcnt<0>();
+      if (stored) wait_vmcnt<MB>();
+      else wait_vmcnt<0>();
     }
     raw_barrier();
   };
@@ -1384,14 +1389,16 @@ __device__ __attribute__((always_inline)) inline void few_quantize(
       nxt = tmp;
       t = tn;
     }
+    bool stored = false;   // the previous iteration stored token tp's codes
     for (int64_t t0 = t_slot0 + stride; t0 < tokens; t0 += stride) {
       const int64_t tn = t + stride;
-      next_x(tn);
+      next_x(tn, stored);
       uint32_t yp[MB][4];
       float amax;
       few_products<DT, MB>(cur, lfrag, rf, lane, yp, amax);
       int32_t* orowp = reinterpret_cast<int32_t*>(out_codes) + tp * (S::F / 8) + 4 * q + lg;
-      if (tp < tokens) few_codes_packed<DT, MB>(ypp, rcpp, orowp, li);
+      stored = tp < tokens;
+      if (stored) few_codes_packed<DT, MB>(ypp, rcpp, orowp, li);
       const float s = few_scale<DT>(amax, red_p, q, lane, clip, amax_d);
       if (q == 0 && lane == 0 && t < tokens) out_scales[t] = s;
       if (tp < tokens && !(sp > 0.f)) few_codes_zero_scale<DT, MB>(ypp, sp, orowp, li);
