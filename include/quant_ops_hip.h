@@ -182,6 +182,32 @@ int qo_w4a4_linear(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
                    void* out, int64_t out_ld, void* stream);
 
 /*
+ * qo_w4a4_linear without caller buffers for the activation codes and scales,
+ * for callers that cannot allocate device memory (HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference, whose apply allocates those intermediates. The codes and scales
+ * go to one staging array per GPU, held from the first call on that GPU until
+ * the process ends, of QO_LINEAR_NOALLOC_MAX_BYTES: tokens * M*N/2 bytes of
+ * codes (rounded up to 256) plus tokens * 4 bytes of scales must fit. Nothing
+ * is allocated per call. Calls that overlap on one GPU (other streams or host
+ * threads) share the array and race. The output equals qo_w4a4_linear's bit
+ * for bit.
+ *
+ * Arguments as qo_w4a4_linear, without codes and act_scales; stream must
+ * belong to the current device.
+ *
+ * Errors: those of qo_w4a4_linear; QO_ERR_SHAPE when the staging does not
+ * fit; QO_ERR_UNSUPPORTED when stream is on another device; QO_ERR_LAUNCH
+ * when the array's address cannot be looked up.
+ */
+#define QO_LINEAR_NOALLOC_MAX_BYTES (32LL * 1024 * 1024)
+int qo_w4a4_linear_noalloc(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
+                           const void* left, const void* right, int M, int N, float clip_ratio,
+                           const int32_t* weight, int64_t weight_ld, int64_t out_features,
+                           const void* weight_scale, int weight_scale_dtype, const void* bias,
+                           void* out, int64_t out_ld, void* stream);
+
+/*
  * Dequantize int4 codes: out[t, f] = float(q[t, f]) * float(scales[t]) (float32).
  *
  * Replaces dequantize_int4 (flatquant/ops.py:156-178), which the reference runs

@@ -20,8 +20,8 @@ STATUS = {0: "QO_OK", 1: "QO_ERR_NULL_POINTER", 2: "QO_ERR_SHAPE", 3: "QO_ERR_DT
 
 # Every symbol the header declares; the CPU tests check they are all exported.
 EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_set_kernel_routing", "qo_flatquant_quantize",
-            "qo_int4_gemm", "qo_int4_gemm_bias", "qo_w4a4_linear", "qo_dequantize_int4", "qo_pack_int4_to_int32",
-            "qo_unpack_int32_to_int4", "qo_transpose_int32")
+            "qo_int4_gemm", "qo_int4_gemm_bias", "qo_w4a4_linear", "qo_w4a4_linear_noalloc", "qo_dequantize_int4",
+            "qo_pack_int4_to_int32", "qo_unpack_int32_to_int4", "qo_transpose_int32")
 
 # QO_ROUTE_* bits of qo_set_kernel_routing (include/quant_ops_hip.h)
 ROUTE = {"FQ_GENERIC": 1 << 0, "FQ_NO_WAVE": 1 << 1, "FQ_NO_DUO": 1 << 2, "FQ_NO_FEW": 1 << 3,
@@ -69,6 +69,9 @@ def lib():
     L.qo_w4a4_linear.restype = c_int
     L.qo_w4a4_linear.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_vp, c_i64, c_i64,
                                  c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]
+    L.qo_w4a4_linear_noalloc.restype = c_int
+    L.qo_w4a4_linear_noalloc.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_vp, c_i64,
+                                         c_i64, c_vp, c_int, c_vp, c_vp, c_i64, c_vp]
     L.qo_dequantize_int4.restype = c_int
     L.qo_dequantize_int4.argtypes = [c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_vp, c_vp]
     for name in ("qo_pack_int4_to_int32", "qo_unpack_int32_to_int4", "qo_transpose_int32"):
@@ -202,6 +205,39 @@ def w4a4_linear(x, left, right, weight, weight_scale, clip_ratio=1.0, bias=None,
         ctypes.c_void_p(codes.data_ptr()), ctypes.c_void_p(scales.data_ptr()),
         ctypes.c_void_p(out.data_ptr()), out.stride(0) if t else no, _stream(stream)))
     return out, codes, scales
+
+
+# Byte size of the staging array of qo_w4a4_linear_noalloc (its header's
+# QO_LINEAR_NOALLOC_MAX_BYTES).
+LINEAR_NOALLOC_MAX_BYTES = 32 * 1024 * 1024
+
+
+def w4a4_linear_noalloc(x, left, right, weight, weight_scale, clip_ratio=1.0, bias=None, out=None, stream=None):
+    """Call ``qo_w4a4_linear_noalloc``: as ``w4a4_linear``, with the activation
+    codes and scales staged in the library's per-GPU array instead of caller
+    buffers (nothing is allocated except ``out`` when it is not given). Returns
+    out [T, out_features] in x's dtype."""
+    t, f = x.shape
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    left, right = left.contiguous(), right.contiguous()
+    if weight.stride(1) != 1:
+        weight = weight.contiguous()
+    weight_scale = weight_scale.reshape(-1).contiguous()
+    m, n = left.shape[0], right.shape[0]
+    no = weight.shape[0]
+    if out is None:
+        out = torch.empty((t, no), dtype=x.dtype, device=x.device)
+    if bias is not None:
+        bias = bias.to(x.dtype).contiguous()
+    _check(lib().qo_w4a4_linear_noalloc(
+        ctypes.c_void_p(x.data_ptr()), _TORCH_CODE[x.dtype], t, x.stride(0) if t else f,
+        ctypes.c_void_p(left.data_ptr()), ctypes.c_void_p(right.data_ptr()), m, n, float(clip_ratio),
+        ctypes.c_void_p(weight.data_ptr()), _ld(weight), no,
+        ctypes.c_void_p(weight_scale.data_ptr()), _TORCH_CODE[weight_scale.dtype],
+        ctypes.c_void_p(bias.data_ptr() if bias is not None else None),
+        ctypes.c_void_p(out.data_ptr()), out.stride(0) if t else no, _stream(stream)))
+    return out
 
 
 def dequantize_int4(codes, scales, packed_int32=False, out=None, stream=None):

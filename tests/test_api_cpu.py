@@ -95,6 +95,19 @@ def test_c_abi_status_and_errors_without_gpu():
     assert st == 1
     assert lib.qo_w4a4_linear(None, 2, 0, 14336, None, None, 112, 128, f, None, 1792, 4096, None, 0, None, None,
                               None, None, 4096, None) == 0
+    # the no-allocation variant: the staging limit and the same argument checks,
+    # all before any device call
+    nl = lib.qo_w4a4_linear_noalloc
+    assert capi.LINEAR_NOALLOC_MAX_BYTES == 32 * 1024 * 1024
+    st = nl(None, 2, 5000, 14336, None, None, 112, 128, f, None, 1792, 4096, None, 0, None, None, 4096, None)
+    assert st == 2 and b"staging" in lib.qo_last_error() and b"qo_w4a4_linear_noalloc" in lib.qo_last_error()
+    st = nl(None, 2, 1 << 40, 14336, None, None, 112, 128, f, None, 1792, 4096, None, 0, None, None, 4096, None)
+    assert st == 2 and b"staging" in lib.qo_last_error()
+    st = nl(None, 2, 4, 12, None, None, 3, 4, f, None, 2, 16, None, 0, None, None, 16, None)
+    assert st == 2 and b"divisible by 8" in lib.qo_last_error()
+    st = nl(None, 2, -1, 14336, None, None, 112, 128, f, None, 1792, 4096, None, 0, None, None, 4096, None)
+    assert st == 2 and b"invalid sizes" in lib.qo_last_error()
+    assert nl(None, 2, 0, 14336, None, None, 112, 128, f, None, 1792, 4096, None, 0, None, None, 4096, None) == 0
     # empty problems are valid no-ops
     assert lib.qo_int4_gemm(None, 1, None, 1, 1, None, 0, None, 0, None, 1, 0, 0, 0, 8, None) == 0
     assert lib.qo_flatquant_quantize(None, 1, 0, 64, None, None, 8, 8, ctypes.c_float(1.0), 1, None, None,
