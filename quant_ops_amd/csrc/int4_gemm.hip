@@ -866,30 +866,32 @@ gemm_i4_skinny(const int32_t* __restrict__ a, int64_t lda, const int32_t* __rest
 // p ^ (r % 16), so the 16 rows of an operand read sit on distinct banks (the
 // DMA's lane -> slot placement is fixed, its source addresses are permuted).
 // Chunks go through a ring of RING buffers behind one barrier each, as the
-// tiled kernels' stages do. SHORT (rows of at most two chunks): a ring of two,
-// every chunk issued at once, and half the LDS, so two workgroups share a CU
-// and one's copies overlap the other's multiply and epilogue.
+// tiled kernels' stages do. PAIR: a ring small enough (<= 80 KiB) for two
+// workgroups to share a CU, so that one's copies overlap the other's multiply
+// and epilogue; the host takes it when the columns need more than one round
+// of workgroups (or a row has at most two chunks, which a ring of two holds
+// whole).
 // ---------------------------------------------------------------------------
-template <int MT, bool SHORT>
+template <int MT, bool PAIR>
 struct SkinnyNkCfg {
   static constexpr int CB = MT == 1 ? 1024 : 512;            // bytes per row per chunk
   static constexpr int SPC = CB / 64, SPW = SPC / 8;         // stages per chunk, per wave
   static constexpr int ROWS = 16 + 16 * MT;
   static constexpr int BUF = ROWS * CB;
-  static constexpr int RING = SHORT ? 2 : 4 * BUF <= 150 * 1024 ? 4 : 3;
+  static constexpr int RING = PAIR ? (3 * BUF <= 80 * 1024 ? 3 : 2) : 4 * BUF <= 150 * 1024 ? 4 : 3;
   static constexpr int NI = BUF / 1024;                      // DMA instructions per chunk
   static constexpr int D = (NI + 7) / 8;                     // ... per wave
   static_assert(SPW >= 1 && D * (RING - 1) < 64, "chunk shape");
-  static_assert(!SHORT || RING == 2, "short rows: one buffer per chunk");
+  static_assert(!PAIR || RING * BUF <= 80 * 1024, "two workgroups per CU");
 };
 
-template <int MT, bool SHORT, class OT>
+template <int MT, bool PAIR, class OT>
 __global__ void __launch_bounds__(512)
 gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
                   const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
                   typename OT::T* __restrict__ out, int64_t ldc, const typename OT::T* __restrict__ bias, int M,
                   int N, int K) {
-  using C = SkinnyNkCfg<MT, SHORT>;
+  using C = SkinnyNkCfg<MT, PAIR>;
   __shared__ __align__(16) unsigned char ring[C::RING * C::BUF];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
@@ -958,15 +960,19 @@ gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __r
     }
   };
 
-  if constexpr (SHORT) {
-    // Every chunk goes out at once, one buffer each; the wait for chunk c
-    // leaves the other in flight only if it was issued.
-    issue(0, 0);
-    if (nch > 1) issue(1, 1);
+  if constexpr (PAIR) {
+    // The RING buffers start empty, so the first RING chunks go out at once;
+    // step c (c >= 1) refills the buffer of chunk c - 1 with chunk c - 1 + RING.
+    // Chunks past the row's end are never issued, so each wait leaves in
+    // flight exactly the chunks issued after chunk c.
+    for (int c = 0; c < C::RING; ++c)
+      if (c < nch) issue(c, c);
     for (int c = 0; c < nch; ++c) {
-      gemm_wait_groups<C::D, 1>(nch - 1 - c);
-      lds_barrier();   // chunk c has landed for every wave
-      compute(c, c);
+      const int last = min(max(c + C::RING - 2, C::RING - 1), nch - 1);   // last chunk issued so far
+      gemm_wait_groups<C::D, C::RING - 1>(last - c);
+      lds_barrier();   // chunk c has landed for every wave; every wave is done with chunk c - 1's buffer
+      if (c > 0 && c - 1 + C::RING < nch) issue(c - 1 + C::RING, (c - 1) % C::RING);
+      compute(c, c % C::RING);
     }
   } else {
     for (int c = 0; c < C::RING - 1; ++c) issue(min(c, nch - 1), c);
@@ -1076,7 +1082,7 @@ static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64
     constexpr int MT = decltype(mt)::value;
     if constexpr (decltype(nk_layout)::value) {
       const int64_t cb = SkinnyNkCfg<MT, false>::CB;
-      if ((K / 2 + cb - 1) / cb <= 2)
+      if ((K / 2 + cb - 1) / cb <= 2 || (N + 15) / 16 > device_cu_count())
         launch((gemm_i4_skinny_nk<MT, true, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb, sbd,
                reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
       else

@@ -567,13 +567,14 @@ def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, routing):
 # Decode shapes (M <= 64): the skinny kernels, every row-block count, K slices
 # of uneven length over the 8 waves (nk % 8 != 0, nk < 8; for M <= 16 with
 # W.t(): chunk counts below, at and above the 8 waves, a partial last chunk;
-# rows of one or two chunks, the two-buffer variant, at every row-block
-# count), ragged N; checked against the oracle and against the tiled kernel on
-# the same inputs.
+# the two-per-CU ring at every row-block count, for rows of at most two chunks
+# and, past one round of workgroups (> 256 column blocks), with refills), ragged
+# N; checked against the oracle and against the tiled kernel on the same inputs.
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 14336), (16, 4096, 14336), (7, 100, 128), (32, 36, 640),
                                    (48, 520, 1152), (64, 64, 4096), (5, 8, 896), (3, 300, 2176),
                                    (16, 40, 15360), (2, 8, 128), (9, 4096, 4096), (64, 200, 1920),
-                                   (20, 96, 2048), (16, 2000, 4096)])
+                                   (20, 96, 2048), (16, 2000, 4096), (32, 4200, 4096), (64, 4160, 5120),
+                                   (16, 4112, 5248), (48, 4400, 1152)])
 @pytest.mark.parametrize("bview", [False, True])
 def test_gemm_skinny_bit_exact(gpu, m, n, k, bview, routing):
     case = wl.gemm_case(m, n, k, seed=5 * m + n + k, b_transposed_view=bview)
