@@ -885,7 +885,7 @@ struct SkinnyNkCfg {
   static_assert(!PAIR || RING * BUF <= 80 * 1024, "two workgroups per CU");
 };
 
-template <int MT, bool PAIR, class OT>
+template <int MT, bool PAIR, bool KN, class OT>
 __global__ void __launch_bounds__(512)
 gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
                   const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
@@ -895,7 +895,13 @@ gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __r
   __shared__ __align__(16) unsigned char ring[C::RING * C::BUF];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int n0 = blockIdx.x * 16;
+  // KN: consecutive column blocks on one XCD (workgroup j runs on XCD j % 8),
+  // so the two 64-byte halves of a 128-byte line of B are read through one L2.
+  // W.t(): block j on XCD j % 8, the placement the linear layer's read-ahead
+  // assumes.
+  const int nblk = gridDim.x;
+  const int cblk = KN && nblk % 8 == 0 ? (blockIdx.x & 7) * (nblk >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int n0 = cblk * 16;
   const int nk = K >> 7;                        // stages
   const int rowbytes = K >> 1;                  // bytes of a packed row
   const int nch = (rowbytes + C::CB - 1) / C::CB;
@@ -912,6 +918,18 @@ gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __r
     return r < 16 ? reinterpret_cast<const char*>(b + (int64_t)min(n0 + r, N - 1) * ldb)
                   : reinterpret_cast<const char*>(a + (int64_t)min(r - 16, M - 1) * lda);
   };
+  // [K/8, N] layout (KN): B instruction i of a chunk copies its stage i, the
+  // 16 packed rows x 64 bytes of columns n0 .. n0 + 15, to 1 KiB of LDS; lane
+  // l fills LDS row position l / 4, piece l % 4 (columns 4 (l % 4) .. + 3).
+  // Packed row 4 g + t of the stage sits at position 4 t + g, so the four rows
+  // an operand read takes (g = 0..3, one t) lie on four distinct bank groups.
+  // Columns past N (N % 4 == 0) re-read the last four; packed rows past K / 8
+  // re-read the last row (never multiplied).
+  const int kn_rows = K >> 3;
+  const uint32_t kn_ld = (uint32_t)ldb * 4u;
+  const uint32_t kn_col = 4u * (uint32_t)min(n0 + 4 * (lane & 3), N - 4);
+  const int kn_row = 4 * ((lane >> 2) & 3) + (lane >> 4);
+  bool kn_b[C::D];
 #pragma unroll
   for (int t = 0; t < C::D; ++t) {
     int i = __builtin_amdgcn_readfirstlane(wave) + 8 * t;
@@ -920,17 +938,24 @@ gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __r
     const int r0 = RPI * i;
     const int r = r0 + (RPI == 2 ? lane >> 5 : 0);
     const int q = RPI == 2 ? lane & 31 : lane;  // LDS slot in the row
+    kn_b[t] = KN && r0 < 16;
     rbase[t] = row_ptr(r0);
     rdiff[t] = (uint32_t)(row_ptr(r) - row_ptr(r0));   // 0 or one row stride (rows clamp monotonically)
-    poff[t] = 16 * (q ^ (r & 15));
+    poff[t] = kn_b[t] ? (uint32_t)(16 * i + kn_row) : 16 * (q ^ (r & 15));   // KN: packed row in the chunk
     ldst[t] = __builtin_amdgcn_readfirstlane(i * 1024);
   }
   auto issue = [&](int c, int buf) {
     const uint32_t base = lds_addr(ring) + buf * C::BUF;
     const uint32_t coff = c * C::CB;
 #pragma unroll
-    for (int t = 0; t < C::D; ++t)   // pieces past the row's end re-read its last piece (never multiplied)
-      dma16_s(rdiff[t] + min(coff + poff[t], (uint32_t)rowbytes - 16), rbase[t], base + ldst[t]);
+    for (int t = 0; t < C::D; ++t) {
+      if (kn_b[t]) {
+        const uint32_t row = min((uint32_t)(c * 16 * C::SPC) + poff[t], (uint32_t)kn_rows - 1);
+        dma16_s(row * kn_ld + kn_col, b, base + ldst[t]);
+      } else {   // pieces past the row's end re-read its last piece (never multiplied)
+        dma16_s(rdiff[t] + min(coff + poff[t], (uint32_t)rowbytes - 16), rbase[t], base + ldst[t]);
+      }
+    }
   };
 
   v4i acc[MT];
@@ -944,7 +969,14 @@ gemm_i4_skinny_nk(const int32_t* __restrict__ a, int64_t lda, const int32_t* __r
       const int ls = wave * C::SPW + u;         // stage within the chunk
       if (c * C::SPC + ls >= nk) break;
       const int slot = (4 * ls + lg) ^ li;
-      const v4i bw = *reinterpret_cast<const v4i*>(base + li * C::CB + 16 * slot);
+      v4i bw;
+      if constexpr (KN) {   // packed rows 4 lg + t of stage ls, column n0 + li
+        const unsigned char* bs = base + ls * 1024 + 64 * lg + 4 * li;
+        bw = v4i{*reinterpret_cast<const int*>(bs), *reinterpret_cast<const int*>(bs + 256),
+                 *reinterpret_cast<const int*>(bs + 512), *reinterpret_cast<const int*>(bs + 768)};
+      } else {
+        bw = *reinterpret_cast<const v4i*>(base + li * C::CB + 16 * slot);
+      }
       v4i aw[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -1078,16 +1110,21 @@ static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64
                           hipStream_t stream) {
   const dim3 grid((unsigned)((N + 15) / 16));
   using T = typename OT::T;
+  // The LDS-DMA kernel for both layouts; [K/8, N] needs whole 4-column groups
+  // and 32-bit byte offsets over B, else the register-streaming kernel.
+  const bool kn_dma = !b_nk && N >= 4 && N % 4 == 0 && ((int64_t)K / 8 - 1) * ldb * 4 + (int64_t)N * 4 < (1LL << 31);
   auto go = [&](auto mt, auto nk_layout) {
     constexpr int MT = decltype(mt)::value;
-    if constexpr (decltype(nk_layout)::value) {
-      const int64_t cb = SkinnyNkCfg<MT, false>::CB;
-      if ((K / 2 + cb - 1) / cb <= 2 || (N + 15) / 16 > device_cu_count())
-        launch((gemm_i4_skinny_nk<MT, true, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb, sbd,
-               reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
+    constexpr bool NK = decltype(nk_layout)::value;
+    const int64_t cb = SkinnyNkCfg<MT, false>::CB;
+    const bool pair = (K / 2 + cb - 1) / cb <= 2 || (N + 15) / 16 > device_cu_count();
+    if (NK || kn_dma) {
+      if (pair)
+        launch((gemm_i4_skinny_nk<MT, true, !NK, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb,
+               sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
       else
-        launch((gemm_i4_skinny_nk<MT, false, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb, sbd,
-               reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
+        launch((gemm_i4_skinny_nk<MT, false, !NK, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb,
+               sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
     } else
       launch((gemm_i4_skinny<decltype(mt)::value, false, OT>), grid, dim3(512), 0, stream, a, lda, b,
                          ldb, sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N,
