@@ -748,7 +748,9 @@ struct SkinnyEpilogue {
 };
 
 // ---------------------------------------------------------------------------
-// Skinny kernel (gemm_i4_skinny): M <= 64, the decode shapes. The time is the
+// Skinny kernel (gemm_i4_skinny): M <= 64, the decode shapes of the [K/8, N]
+// layout that the LDS-DMA kernel below does not take (N % 4 != 0 with a padded
+// row stride, or B beyond 32-bit byte offsets). The time is the
 // read of B, so the work is spread over columns and K instead of tiles: a
 // workgroup owns 16 output columns and all M rows; its 8 waves split K into
 // contiguous slices of 128-deep stages, stream their slice of B and A from
@@ -854,7 +856,8 @@ gemm_i4_skinny(const int32_t* __restrict__ a, int64_t lda, const int32_t* __rest
 
 // ---------------------------------------------------------------------------
 // Skinny kernel for the W.t() layout (gemm_i4_skinny_nk), the decode GEMM of
-// the linear layer. Same split as gemm_i4_skinny (16 output columns and all M
+// the linear layer, and (KN) for the [K/8, N] layout, whose B copies differ
+// (see the KN set-up below). Same split as gemm_i4_skinny (16 output columns and all M
 // rows per workgroup, exact int32 sums of per-wave partials through LDS), but
 // A and B reach LDS by LDS-DMA in "chunks" of CB contiguous bytes of every
 // row (the 16 B rows = columns n0 .. n0 + 15, then the 16 MT rows of A): each
