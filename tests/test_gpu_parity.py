@@ -593,6 +593,24 @@ def test_gemm_skinny_bit_exact(gpu, m, n, k, bview, routing):
     assert torch.equal(out, out_tiled)
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 1030, 1024), (5, 6, 256), (40, 301, 2048)])
+def test_gemm_skinny_kn_padded_rows(gpu, m, n, k):
+    """[K/8, N] B with N % 4 != 0 in rows padded to a multiple of 4 words (and
+    a padded output): the register-streaming decode kernel, which takes the
+    shapes whose 4-column groups the LDS-DMA kernel cannot copy whole."""
+    case = wl.gemm_case(m, n, k, seed=3 * m + n + k)
+    _say(f"gemm skinny KN padded {m}x{n}x{k}")
+    ldb = (n + 3) // 4 * 4 + 4
+    store = torch.zeros(k // 8, ldb, dtype=torch.int32)
+    store[:, :n] = case.b
+    b = store.to(gpu)[:, :n]
+    out_store = torch.empty(m, ldb, dtype=torch.bfloat16, device=gpu)
+    out = capi.int4_gemm(case.a.to(gpu), b, case.scale_a.to(gpu), case.scale_b.to(gpu), out=out_store[:, :n])
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b,
+                                                          out_dtype=torch.bfloat16))
+
+
 @pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
 def test_gemm_decode_scale_dtypes_and_bias(gpu, sdt, odt):
