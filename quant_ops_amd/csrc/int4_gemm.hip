@@ -881,11 +881,13 @@ struct SkinnyNkCfg {
   static constexpr int SPC = CB / 64, SPW = SPC / 8;         // stages per chunk, per wave
   static constexpr int ROWS = 16 + 16 * MT;
   static constexpr int BUF = ROWS * CB;
-  static constexpr int RING = PAIR ? (3 * BUF <= 80 * 1024 ? 3 : 2) : 4 * BUF <= 150 * 1024 ? 4 : 3;
+  static constexpr bool PAIR_OK = 2 * BUF <= 80 * 1024;     // a two-per-CU ring exists (M <= 64)
+  static constexpr int RING = PAIR ? (3 * BUF <= 80 * 1024 ? 3 : 2)
+                                   : 4 * BUF <= 150 * 1024 ? 4 : 3 * BUF <= 150 * 1024 ? 3 : 2;
   static constexpr int NI = BUF / 1024;                      // DMA instructions per chunk
   static constexpr int D = (NI + 7) / 8;                     // ... per wave
-  static_assert(SPW >= 1 && D * (RING - 1) < 64, "chunk shape");
-  static_assert(!PAIR || RING * BUF <= 80 * 1024, "two workgroups per CU");
+  static_assert(SPW >= 1 && D * (RING - 1) < 64 && MT <= 8, "chunk shape");
+  static_assert(!PAIR || (PAIR_OK && RING * BUF <= 80 * 1024), "two workgroups per CU");
 };
 
 template <int MT, bool PAIR, bool KN, class OT>
@@ -1107,6 +1109,10 @@ static bool gemm_allow_skinny() {
   return !route_off(QO_ROUTE_GEMM_NO_SKINNY);
 }
 
+static bool skinny_kn_dma_ok(int64_t N, int64_t K, int64_t ldb) {
+  return N >= 4 && N % 4 == 0 && (K / 8 - 1) * ldb * 4 + N * 4 < (1LL << 31);
+}
+
 template <class OT>
 static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, bool b_nk, const void* sa,
                           int sad, const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K,
@@ -1115,23 +1121,29 @@ static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64
   using T = typename OT::T;
   // The LDS-DMA kernel for both layouts; [K/8, N] needs whole 4-column groups
   // and 32-bit byte offsets over B, else the register-streaming kernel.
-  const bool kn_dma = !b_nk && N >= 4 && N % 4 == 0 && ((int64_t)K / 8 - 1) * ldb * 4 + (int64_t)N * 4 < (1LL << 31);
+  const bool kn_dma = !b_nk && skinny_kn_dma_ok(N, K, ldb);
   auto go = [&](auto mt, auto nk_layout) {
     constexpr int MT = decltype(mt)::value;
     constexpr bool NK = decltype(nk_layout)::value;
-    const int64_t cb = SkinnyNkCfg<MT, false>::CB;
+    using Cfg = SkinnyNkCfg<MT, false>;
+    const int64_t cb = Cfg::CB;
     const bool pair = (K / 2 + cb - 1) / cb <= 2 || (N + 15) / 16 > device_cu_count();
     if (NK || kn_dma) {
-      if (pair)
-        launch((gemm_i4_skinny_nk<MT, true, !NK, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb,
-               sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
-      else
+      bool launched = false;
+      if constexpr (Cfg::PAIR_OK) {
+        if (pair) {
+          launch((gemm_i4_skinny_nk<MT, true, !NK, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb,
+                 sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
+          launched = true;
+        }
+      }
+      if (!launched)
         launch((gemm_i4_skinny_nk<MT, false, !NK, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb,
                sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
-    } else
-      launch((gemm_i4_skinny<decltype(mt)::value, false, OT>), grid, dim3(512), 0, stream, a, lda, b,
-                         ldb, sa, sad, sb, sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N,
-                         K);
+    } else if constexpr (MT <= 4) {   // the host sends M > 64 here only for the LDS-DMA kernel
+      launch((gemm_i4_skinny<MT, false, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb, sbd,
+             reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
+    }
   };
   auto by_layout = [&](auto mt) {
     if (b_nk) go(mt, std::true_type{});
@@ -1141,7 +1153,11 @@ static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64
   if (mt == 1) by_layout(std::integral_constant<int, 1>{});
   else if (mt == 2) by_layout(std::integral_constant<int, 2>{});
   else if (mt == 3) by_layout(std::integral_constant<int, 3>{});
-  else by_layout(std::integral_constant<int, 4>{});
+  else if (mt == 4) by_layout(std::integral_constant<int, 4>{});
+  else if (mt == 5) by_layout(std::integral_constant<int, 5>{});
+  else if (mt == 6) by_layout(std::integral_constant<int, 6>{});
+  else if (mt == 7) by_layout(std::integral_constant<int, 7>{});
+  else by_layout(std::integral_constant<int, 8>{});
 }
 
 template <class OT>
@@ -1159,9 +1175,27 @@ static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bs
                        ((uintptr_t)out % (4 * sizeof(T)) == 0) && (ldc % 4 == 0);
   if (allow_fast && fits && aligned && (b_nk || b_kn)) {
     const int m = (int)M, n = (int)N, k = (int)K;
-    // decode shapes: the skinny kernel (columns x K-slices, B streamed once)
-    if (m <= 64 && k % 128 == 0 && k > 0 && gemm_allow_skinny()) {
+    // decode shapes: the skinny kernel (columns x K-slices, B streamed once);
+    // up to 128 rows where its LDS-DMA form takes the layout (one round of
+    // 256-row tiles would leave most CUs idle and stream all of K per tile)
+    const bool dma_layout = b_nk || skinny_kn_dma_ok(n, k, ldb);
+    const bool skinny_rows = m <= 64 || (m <= 128 && dma_layout);
+    if (skinny_rows && k % 128 == 0 && k > 0 && gemm_allow_skinny()) {
       launch_skinny<OT>(a, lda, b, ldb, b_nk, sa, sad, sb, sbd, out, ldc, bias, m, n, k, stream);
+      return;
+    }
+    // Up to 512 rows over few columns (the tiled grid would fill at most 1/8
+    // of the CUs, each tile streaming all of K): one skinny launch per 128
+    // rows. Measured at 128 x 4096 x 14336: 27 us per launch against 134 us
+    // for the tiled kernel at any M up to 256.
+    const int64_t tiles = (int64_t)((m + 255) / 256) * ((n + 255) / 256);
+    if (m <= 512 && dma_layout && tiles * 8 <= device_cu_count() && k % 128 == 0 && k > 0 &&
+        gemm_allow_skinny()) {
+      const int sa_size = sad == QO_DTYPE_F32 ? 4 : 2;
+      for (int r0 = 0; r0 < m; r0 += 128)
+        launch_skinny<OT>(a + (int64_t)r0 * lda, lda, b, ldb, b_nk,
+                          static_cast<const char*>(sa) + (int64_t)r0 * sa_size, sad, sb, sbd,
+                          reinterpret_cast<T*>(out) + (int64_t)r0 * ldc, ldc, bias, min(128, m - r0), n, k, stream);
       return;
     }
     // pipelined kernel: whole 128-deep stages; KN rows read as 16-byte column groups

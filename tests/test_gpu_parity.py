@@ -564,7 +564,9 @@ def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, routing):
     assert torch.equal(out, out_old)
 
 
-# Decode shapes (M <= 64): the skinny kernels, every row-block count, K slices
+# Decode shapes (M <= 64, up to 128 rows on the LDS-DMA kernel, and 129-512
+# rows over few columns as one launch per 128 rows): the skinny kernels, every
+# row-block count, K slices
 # of uneven length over the 8 waves (nk % 8 != 0, nk < 8; for M <= 16 with
 # W.t(): chunk counts below, at and above the 8 waves, a partial last chunk;
 # the two-per-CU ring at every row-block count, for rows of at most two chunks
@@ -574,7 +576,9 @@ def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, routing):
                                    (48, 520, 1152), (64, 64, 4096), (5, 8, 896), (3, 300, 2176),
                                    (16, 40, 15360), (2, 8, 128), (9, 4096, 4096), (64, 200, 1920),
                                    (20, 96, 2048), (16, 2000, 4096), (32, 4200, 4096), (64, 4160, 5120),
-                                   (16, 4112, 5248), (48, 4400, 1152)])
+                                   (16, 4112, 5248), (48, 4400, 1152), (80, 1000, 4096), (128, 300, 1024),
+                                   (100, 520, 14336), (72, 36, 640), (128, 4112, 1152), (113, 64, 2176),
+                                   (200, 300, 2048), (256, 520, 4096), (384, 4096, 1024), (129, 64, 128)])
 @pytest.mark.parametrize("bview", [False, True])
 def test_gemm_skinny_bit_exact(gpu, m, n, k, bview, routing):
     case = wl.gemm_case(m, n, k, seed=5 * m + n + k, b_transposed_view=bview)
@@ -609,6 +613,27 @@ def test_gemm_skinny_kn_padded_rows(gpu, m, n, k):
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), oi4.int4_matmul_pytorch(case.a, case.b, case.scale_a, case.scale_b,
                                                           out_dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("sdt", [torch.float32, torch.bfloat16])
+def test_gemm_row_split_scales_and_bias(gpu, sdt):
+    """300 rows over 272 columns run as three 128-row skinny launches: each
+    launch's token scales start at its first row (float32 and 16-bit scales),
+    with a bias; bit-exact against the tiled kernel and the fallback."""
+    m, n, k = 300, 272, 1024
+    case = wl.gemm_case(m, n, k, seed=29, b_transposed_view=True)
+    _say(f"gemm row split {m}x{n}x{k} scales {sdt}")
+    sa, sb = case.scale_a.to(sdt), case.scale_b.to(sdt)
+    g = torch.Generator().manual_seed(30)
+    bias = (torch.randn(n, generator=g) * 0.5).to(torch.bfloat16)
+    a, b = case.a.to(gpu), case.b.to(gpu)
+    out = capi.int4_gemm(a, b, sa.to(gpu), sb.to(gpu), out_dtype=torch.bfloat16, bias=bias.to(gpu))
+    with capi.kernel_routing("GEMM_NO_SKINNY"):
+        out_tiled = capi.int4_gemm(a, b, sa.to(gpu), sb.to(gpu), out_dtype=torch.bfloat16, bias=bias.to(gpu))
+    torch.cuda.synchronize()
+    ref = oi4.int4_matmul_pytorch(case.a, case.b, sa, sb, out_dtype=torch.bfloat16)
+    assert torch.equal(out, out_tiled)
+    assert torch.equal(out.cpu(), ref + bias)
 
 
 @pytest.mark.parametrize("sdt", [torch.float32, torch.float16, torch.bfloat16])
