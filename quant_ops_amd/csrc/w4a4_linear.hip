@@ -8,7 +8,8 @@
 // Largest token count whose linear call reads the weight ahead: the small-M
 // GEMM's range. Measured on 112 x 128 -> 4096 x 14336 bf16 (step, same
 // process): 1 token 15.68 -> 15.41 us, 16 tokens 16.70 -> 16.02, 32 tokens
-// 17.95 -> 17.34, 64 tokens 21.44 -> 20.69.
+// 17.95 -> 17.34, 64 tokens 21.44 -> 20.69; at 96 and 128 tokens (the GEMM
+// no longer waits on the weight) 26.7 and 29.7 us either way.
 constexpr int64_t kReadAheadTokens = 64;
 
 static int linear_run(const char* fn, const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
