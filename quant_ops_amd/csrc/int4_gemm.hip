@@ -654,7 +654,7 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
   static_assert(BM <= 256 && BN <= 64 * W - 256, "one scale per thread");
   float sv = 0.f, bv = 0.f;
   if (tid < BM) sv = load_scale(sa, sad, min(m0 + tid, M - 1));
-  else if (tid - 256 < BN) {
+  else if (tid >= 256 && tid - 256 < BN) {   // threads 256 .. 256 + BN - 1 (any BM <= 256)
     sv = load_scale(sb, sbd, min(n0 + tid - 256, N - 1));
     if (bias) bv = (float)bias[min(n0 + tid - 256, N - 1)];
   }
@@ -664,7 +664,7 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
   if constexpr (STAGES > 3) issue(min(3, nk - 1), std::integral_constant<int, 3>{});
   gemm_wait_vmcnt<PER * (STAGES - 1)>();
   if (tid < BM) s_sa[tid] = sv;
-  else if (tid - 256 < BN) {
+  else if (tid >= 256 && tid - 256 < BN) {
     s_sb[tid - 256] = sv;
     s_bias[tid - 256] = bv;
   }
@@ -1097,7 +1097,12 @@ template <bool B_NK, class OT>
 static void dispatch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
                          const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K, hipStream_t stream) {
   const int cus = device_cu_count();
-  if (tile_efficiency(M, N, 256, 224, cus) > tile_efficiency(M, N, 256, 256, cus))
+  const double e224 = tile_efficiency(M, N, 256, 224, cus), e256 = tile_efficiency(M, N, 256, 256, cus);
+  // Under half a round of 256-row tiles (M of a few hundred rows over many
+  // columns): 128 x 128 tiles, four times as many, two workgroups per CU.
+  if (std::max(e224, e256) < 0.5)
+    launch_dma<128, 128, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
+  else if (e224 > e256)
     launch_dma<256, 224, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
   else
     launch_dma<256, 256, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
