@@ -1191,12 +1191,13 @@ static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bs
       launch_skinny<OT>(a, lda, b, ldb, b_nk, sa, sad, sb, sbd, out, ldc, bias, m, n, k, stream);
       return;
     }
-    // Up to 512 rows over few columns (the tiled grid would fill at most 1/8
+    // Up to 256 rows over few columns (the tiled grid would fill at most 1/8
     // of the CUs, each tile streaming all of K): one skinny launch per 128
-    // rows. Measured at 128 x 4096 x 14336: 27 us per launch against 134 us
-    // for the tiled kernel at any M up to 256.
+    // rows. Measured at N x K = 4096 x 14336, M = 200 / 256 / 512: 42.0 /
+    // 51.6 / 101.6 us this way, 62.1 / 66.1 / 65.3 us on 128 x 128 tiles,
+    // 137.7 / 139.0 / 138.0 us on 256-row tiles.
     const int64_t tiles = (int64_t)((m + 255) / 256) * ((n + 255) / 256);
-    if (m <= 512 && dma_layout && tiles * 8 <= device_cu_count() && k % 128 == 0 && k > 0 &&
+    if (m <= 256 && dma_layout && tiles * 8 <= device_cu_count() && k % 128 == 0 && k > 0 &&
         gemm_allow_skinny()) {
       const int sa_size = sad == QO_DTYPE_F32 ? 4 : 2;
       for (int r0 = 0; r0 < m; r0 += 128)

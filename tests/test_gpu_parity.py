@@ -564,7 +564,7 @@ def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, routing):
     assert torch.equal(out, out_old)
 
 
-# Decode shapes (M <= 64, up to 128 rows on the LDS-DMA kernel, and 129-512
+# Decode shapes (M <= 64, up to 128 rows on the LDS-DMA kernel, and 129-256
 # rows over few columns as one launch per 128 rows): the skinny kernels, every
 # row-block count, K slices
 # of uneven length over the 8 waves (nk % 8 != 0, nk < 8; for M <= 16 with
