@@ -928,10 +928,12 @@ def test_linear_read_ahead_changes_nothing(gpu, tokens, m, out_f, pad):
 
 
 @pytest.mark.parametrize("tokens,m,n,dtype", [(17, 112, 128, torch.bfloat16), (40, 64, 64, torch.float16),
-                                              (4, 96, 96, torch.bfloat16), (8, 32, 64, torch.float32)])
+                                              (4, 96, 96, torch.bfloat16), (8, 32, 64, torch.float32),
+                                              (100, 112, 128, torch.bfloat16), (200, 64, 128, torch.float16)])
 def test_linear_entry_point_other_sizes(gpu, tokens, m, n, dtype):
-    """Other shapes and dtypes (more tokens, N != 128, float32 x) through the
-    entry point against the oracle."""
+    """Other shapes and dtypes (more tokens, N != 128, float32 x; 100 tokens on
+    the skinny GEMM's 7 row blocks, 200 tokens as two row-split launches)
+    through the entry point against the oracle."""
     out_f = 272
     x, L, R, w, sw, bias = _linear_inputs(tokens, m, n, out_f, dtype, 77 + tokens)
     _say(f"linear T={tokens} {m}x{n} {dtype}")
