@@ -1182,20 +1182,19 @@ static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bs
                        ((uintptr_t)out % (4 * sizeof(T)) == 0) && (ldc % 4 == 0);
   if (allow_fast && fits && aligned && (b_nk || b_kn)) {
     const int m = (int)M, n = (int)N, k = (int)K;
-    // decode shapes: the skinny kernel (columns x K-slices, B streamed once);
-    // up to 128 rows where its LDS-DMA form takes the layout (one round of
-    // 256-row tiles would leave most CUs idle and stream all of K per tile)
+    // decode shapes: the skinny kernel (columns x K-slices, B streamed once)
     const bool dma_layout = b_nk || skinny_kn_dma_ok(n, k, ldb);
-    const bool skinny_rows = m <= 64 || (m <= 128 && dma_layout);
-    if (skinny_rows && k % 128 == 0 && k > 0 && gemm_allow_skinny()) {
+    if (m <= 64 && k % 128 == 0 && k > 0 && gemm_allow_skinny()) {
       launch_skinny<OT>(a, lda, b, ldb, b_nk, sa, sad, sb, sbd, out, ldc, bias, m, n, k, stream);
       return;
     }
     // Up to 256 rows over few columns (the tiled grid would fill at most 1/8
     // of the CUs, each tile streaming all of K): one skinny launch per 128
-    // rows. Measured at N x K = 4096 x 14336, M = 200 / 256 / 512: 42.0 /
-    // 51.6 / 101.6 us this way, 62.1 / 66.1 / 65.3 us on 128 x 128 tiles,
-    // 137.7 / 139.0 / 138.0 us on 256-row tiles.
+    // rows. Measured at N x K = 4096 x 14336, M = 128 / 200 / 256 / 512:
+    // 26.8 / 42.0 / 51.6 / 101.6 us this way, - / 62.1 / 66.1 / 65.3 us on
+    // 128 x 128 tiles, 133.7 / 137.7 / 139.0 / 138.0 us on 256-row tiles.
+    // Over many columns the 128 x 128 tiles win from 65 rows (14336 x 4096,
+    // M = 80 / 128: 21.1 / 24.1 us against 27.9 / 36.6 us skinny).
     const int64_t tiles = (int64_t)((m + 255) / 256) * ((n + 255) / 256);
     if (m <= 256 && dma_layout && tiles * 8 <= device_cu_count() && k % 128 == 0 && k > 0 &&
         gemm_allow_skinny()) {

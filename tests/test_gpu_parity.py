@@ -546,7 +546,8 @@ def test_gemm_small_bit_exact(gpu, m, n, k, bview):
 # several tile sizes, both B layouts; cross-checked against the oracle and the
 # register-staged kernel.
 @pytest.mark.parametrize("m,n,k", [(1, 4, 128), (16, 16, 128), (300, 260, 1024), (257, 516, 2048),
-                                   (512, 448, 512), (256, 224, 384), (33, 12, 256), (1024, 1792, 1152)])
+                                   (512, 448, 512), (256, 224, 384), (33, 12, 256), (1024, 1792, 1152),
+                                   (96, 9000, 1024), (200, 8200, 640)])
 @pytest.mark.parametrize("bview", [False, True])
 def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, routing):
     case = wl.gemm_case(m, n, k, seed=3 * m + n + k, b_transposed_view=bview)
@@ -564,8 +565,8 @@ def test_gemm_pipelined_bit_exact(gpu, m, n, k, bview, routing):
     assert torch.equal(out, out_old)
 
 
-# Decode shapes (M <= 64, up to 128 rows on the LDS-DMA kernel, and 129-256
-# rows over few columns as one launch per 128 rows): the skinny kernels, every
+# Decode shapes (M <= 64, and up to 256 rows over few columns as one LDS-DMA
+# launch per 128 rows, up to 8 row blocks each): the skinny kernels, every
 # row-block count, K slices
 # of uneven length over the 8 waves (nk % 8 != 0, nk < 8; for M <= 16 with
 # W.t(): chunk counts below, at and above the 8 waves, a partial last chunk;
