@@ -1147,9 +1147,13 @@ static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64
       if (!launched)
         launch((gemm_i4_skinny_nk<MT, false, !NK, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb,
                sbd, reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
-    } else if constexpr (MT <= 4) {   // the host sends M > 64 here only for the LDS-DMA kernel
+    } else if constexpr (MT <= 4) {
       launch((gemm_i4_skinny<MT, false, OT>), grid, dim3(512), 0, stream, a, lda, b, ldb, sa, sad, sb, sbd,
              reinterpret_cast<T*>(out), ldc, reinterpret_cast<const T*>(bias), M, N, K);
+    } else if (g_launch_error == hipSuccess) {
+      // M > 64 comes here only with a layout the LDS-DMA kernel takes; report
+      // rather than leave the output unwritten if that ever changes
+      g_launch_error = hipErrorInvalidConfiguration;
     }
   };
   auto by_layout = [&](auto mt) {
