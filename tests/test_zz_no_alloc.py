@@ -43,6 +43,20 @@ def test_linear_noalloc_matches_linear(gpu):
         assert torch.equal(y, y_ref), f"call {i}: noalloc output differs from qo_w4a4_linear"
 
 
+def test_linear_noalloc_on_a_side_stream(gpu):
+    # a non-null stream of the current device (its device is checked), after
+    # the calls above left the staging array holding other codes
+    x, L, R, w, sw, bias = _inputs(12, 112, 128, 1000, torch.bfloat16, 950, True)
+    xd, Ld, Rd, wd, swd, bd = (t.to(gpu) for t in (x, L, R, w, sw, bias))
+    y_ref, _, _ = capi.w4a4_linear(xd, Ld, Rd, wd, swd, 0.9, bd)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        y = capi.w4a4_linear_noalloc(xd, Ld, Rd, wd, swd, 0.9, bd)
+    side.synchronize()
+    assert torch.equal(y, y_ref)
+
+
 def test_linear_noalloc_rejects_oversize(gpu):
     # staging need above the limit: 5000 tokens x 14336 features (35.8 MB of codes)
     x = torch.zeros(5000, 14336, dtype=torch.bfloat16, device=gpu)
