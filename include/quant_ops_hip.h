@@ -193,6 +193,10 @@ int qo_w4a4_linear(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
  * threads) share the array and race. The output equals qo_w4a4_linear's bit
  * for bit.
  *
+ * The array's device address is looked up (hipGetSymbolAddress) on the
+ * first call on each GPU and kept for the life of the process, so a device
+ * reset (hipDeviceReset) between calls is not supported.
+ *
  * Arguments as qo_w4a4_linear, without codes and act_scales; stream must
  * belong to the current device.
  *

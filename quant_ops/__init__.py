@@ -12,7 +12,6 @@ library and define the ``quant_ops::*`` schemas), the fake kernels, then the
 availability flag.
 """
 __version__ = "0.1.0"
-__author__ = "Quant Ops Team"
 
 from .ops.quantization.flatquant import dequantize_int4, flatquant_dynamic_quantize
 from .ops.quantization.int4_matmul.ops import int4_matmul

@@ -1,6 +1,8 @@
 // C ABI of the W4A4 FlatQuant linear layer: quantize (packed codes) then the
 // GEMM against the weight's transposed view, bias in the GEMM epilogue, as the
 // kernels of qo_flatquant_quantize and qo_int4_gemm(_bias) on one stream.
+#include <stdio.h>
+
 #include <mutex>
 
 #include "common.h"
@@ -11,6 +13,15 @@
 // 17.95 -> 17.34, 64 tokens 21.44 -> 20.69; at 96 and 128 tokens (the GEMM
 // no longer waits on the weight) 26.7 and 29.7 us either way.
 constexpr int64_t kReadAheadTokens = 64;
+
+// A failure of the quantize or GEMM stage of a linear call: the stage's
+// message, prefixed with the entry point the caller called, and its status.
+static int inner_failed(const char* fn, int status) {
+  char inner[512];
+  snprintf(inner, sizeof(inner), "%s", qo_last_error());
+  qo_set_error("%s: %s", fn, inner);
+  return status;
+}
 
 static int linear_run(const char* fn, const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
                       const void* right, int M, int N, float clip_ratio, const int32_t* weight, int64_t weight_ld,
@@ -60,12 +71,13 @@ static int linear_run(const char* fn, const void* x, int x_dtype, int64_t tokens
   }
   const int q = flatquant_quantize(x, x_dtype, tokens, x_ld, left, right, M, N, clip_ratio, 1, codes, act_scales,
                                    stream, ahead);
-  if (q != QO_OK) return q;
-  return bias ? qo_int4_gemm_bias(codes, features / 8, weight, 1, weight_ld, act_scales, QO_DTYPE_F32, weight_scale,
-                                  weight_scale_dtype, bias, out, x_dtype, out_ld, tokens, out_features, features,
-                                  stream)
-              : qo_int4_gemm(codes, features / 8, weight, 1, weight_ld, act_scales, QO_DTYPE_F32, weight_scale,
-                             weight_scale_dtype, out, x_dtype, out_ld, tokens, out_features, features, stream);
+  if (q != QO_OK) return inner_failed(fn, q);
+  const int g = bias ? qo_int4_gemm_bias(codes, features / 8, weight, 1, weight_ld, act_scales, QO_DTYPE_F32,
+                                         weight_scale, weight_scale_dtype, bias, out, x_dtype, out_ld, tokens,
+                                         out_features, features, stream)
+                     : qo_int4_gemm(codes, features / 8, weight, 1, weight_ld, act_scales, QO_DTYPE_F32, weight_scale,
+                                    weight_scale_dtype, out, x_dtype, out_ld, tokens, out_features, features, stream);
+  return g == QO_OK ? g : inner_failed(fn, g);
 }
 
 extern "C" int qo_w4a4_linear(const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
