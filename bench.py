@@ -35,6 +35,7 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--warm-s 0.2] [--no
        python bench.py --pmc-pass                       (under rocprofv3 --pmc FETCH_SIZE or WRITE_SIZE)
        python bench.py --pmc-summary FETCH_DIR WRITE_DIR
        python bench.py --pmc-table PMC_DIR [PMC_DIR ...]
+       python bench.py --ceilings                       (int8 MFMA rate, empty launch, streaming copy)
        python bench.py --trace-summary KERNEL_TRACE_CSV [--trace-last K]
                                                         (rocprofv3 --kernel-trace --output-format csv)
 """
@@ -692,6 +693,63 @@ def _traffic_from_profiles(kernel_key):
         return None
 
 
+# --------------------------------------------------------------------------- ceilings
+
+def ceilings(torch, steps, warmup, dev):
+    """Microbenchmarks of the ceilings the kernels are compared with
+    (libquant_ops_probes.so): the int8 MFMA rate with 0-8 independent VALU
+    instructions per MFMA (two waves per SIMD on every CU), an empty kernel's
+    launch in a graph, and a streaming kernel moving config 2's bytes (16.8 MB
+    in, 4.2 MB out). Each is timed like the workloads (graph of ``steps``
+    launches, HIP events); one JSON line."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "quant_ops_amd", "libquant_ops_probes.so"))
+    c_vp, c_int, c_i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    lib.qo_probe_mfma_i8.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_int]
+    lib.qo_probe_empty.argtypes = [c_vp]
+    lib.qo_probe_stream.argtypes = [c_vp, c_vp, c_i64, c_int, c_vp]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {"cus": cus}
+    sink = torch.empty(cus * 512, dtype=torch.int32, device=dev)
+    iters = 4096
+    for threads, key in ((512, "mfma_i8"), (256, "mfma_i8_one_wave_per_simd")):
+        mfma = {}
+        for kv in (0, 1, 2, 3, 4, 8):
+            def launch(i, kv=kv, threads=threads):
+                assert lib.qo_probe_mfma_i8(kv, cus, iters, ctypes.c_void_p(sink.data_ptr()), stream(), threads) == 0
+            ms, _ = _time_graph(torch, launch, steps, warmup)
+            ops = 2 * 16 * 16 * 64 * 8 * iters * (threads // 64) * cus   # per MFMA x MFMAs per wave x waves
+            mfma[f"valu_per_mfma_{kv}"] = {"us_per_launch": ms / steps * 1e3, "TOPS": ops / (ms / steps * 1e-3) / 1e12}
+            _log(f"ceiling: int8 MFMA, {threads // 256} wave(s) per SIMD, {kv} VALU per MFMA: "
+                 f"{mfma[f'valu_per_mfma_{kv}']['TOPS']:.0f} TOP/s")
+        out[key] = mfma
+
+    def launch_empty(i):
+        assert lib.qo_probe_empty(stream()) == 0
+    ms, _ = _time_graph(torch, launch_empty, steps, warmup)
+    out["empty_kernel_us"] = ms / steps * 1e3
+    _log(f"ceiling: empty kernel {out['empty_kernel_us']:.2f} us per launch in a graph")
+
+    bytes_in = 2048 * 4096 * 2
+    nsets = _nsets(bytes_in * 5 // 4, steps)
+    ins = [torch.empty(bytes_in // 4, dtype=torch.int32, device=dev).fill_(i) for i in range(nsets)]
+    outs = [torch.empty(bytes_in // 16, dtype=torch.int32, device=dev) for _ in range(nsets)]
+    stream_res = {}
+    for blocks in (1024, 4096, 16384):
+        def launch_stream(i, blocks=blocks):
+            j = i % nsets
+            assert lib.qo_probe_stream(ctypes.c_void_p(ins[j].data_ptr()), ctypes.c_void_p(outs[j].data_ptr()),
+                                       bytes_in, blocks, stream()) == 0
+        ms, _ = _time_graph(torch, launch_stream, steps, warmup)
+        us = ms / steps * 1e3
+        stream_res[f"blocks_{blocks}"] = {"us_per_launch": us, "GBps": bytes_in * 5 / 4 / (us * 1e-6) / 1e9}
+        _log(f"ceiling: stream of config 2's bytes, {blocks} blocks: {us:.2f} us")
+    out["stream_cfg2_bytes"] = stream_res
+    print(json.dumps({"ceilings": out}), flush=True)
+
+
 # --------------------------------------------------------------------------- main
 
 def main():
@@ -714,6 +772,8 @@ def main():
                     help="print per-launch HBM bytes from two rocprofv3 --pmc output folders")
     ap.add_argument("--pmc-table", nargs="+", metavar="PMC_DIR",
                     help="per-kernel medians of every counter in rocprofv3 --pmc output folders of --pmc-pass")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="microbenchmarks of the int8 MFMA rate, an empty launch and a streaming copy")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
@@ -748,6 +808,9 @@ def main():
     dev = torch.device("cuda", 0)
     if args.pmc_pass:
         pmc_pass(torch, dev)
+        return
+    if args.ceilings:
+        ceilings(torch, args.steps, args.warmup, dev)
         return
     steps, warmup = args.steps, args.warmup
 

@@ -5,7 +5,9 @@ Produces, in-tree next to this file:
 * ``libquant_ops_hip.so`` — the gfx950 HIP kernels behind the C ABI declared in
   ``include/quant_ops_hip.h`` (no torch dependency);
 * ``_quant_ops_torch.so`` — the torch operator registration (``quant_ops::*``)
-  that calls that C ABI, linked against it with an ``$ORIGIN`` rpath.
+  that calls that C ABI, linked against it with an ``$ORIGIN`` rpath;
+* ``libquant_ops_probes.so`` — microbenchmarks of the hardware ceilings
+  (``bench.py --ceilings``), kept out of the product library.
 
 ``hipcc`` cross-compiles for gfx950 without a GPU. Every HIP file is built
 with packed fp32 instructions disabled.
@@ -27,6 +29,9 @@ OBJ = os.path.join(HERE, "_obj")
 HIP_SOURCES = ["capi.hip", "flatquant_quant.hip", "int4_gemm.hip", "dequant.hip", "layout.hip", "w4a4_linear.hip"]
 LIB_NAME = "libquant_ops_hip.so"
 TORCH_LIB_NAME = "_quant_ops_torch.so"
+# microbenchmarks of the hardware ceilings (bench.py --ceilings), a library of its own
+PROBE_SOURCE = "probes.hip"
+PROBE_LIB_NAME = "libquant_ops_probes.so"
 
 ARCH = os.environ.get("QUANT_OPS_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
@@ -109,10 +114,22 @@ def build_torch_binding(verbose=True):
     return out
 
 
+def build_probe_library(verbose=True):
+    os.makedirs(OBJ, exist_ok=True)
+    out = os.path.join(HERE, PROBE_LIB_NAME)
+    tmp = out + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, PROBE_SOURCE), "-o", tmp])
+    os.replace(tmp, out)
+    if verbose:
+        print(f"[quant_ops_amd] built {out}")
+    return out
+
+
 def build(verbose=True):
     """Compile every native part (always recompiles)."""
     build_hip_library(verbose)
     build_torch_binding(verbose)
+    build_probe_library(verbose)
 
 
 if __name__ == "__main__":

@@ -7,8 +7,9 @@
 // integers is exact, then two separate float32 products, then one rounding.
 //
 // MFMA kernels: gfx950 has no int4 MFMA, so nibbles are widened to int8 and
-// fed to v_mfma_i32_16x16x64_i8. gemm_i4_pp (K % 128 == 0, the main path)
-// stages packed words in LDS and widens after the LDS read; gemm_i4_mfma
+// fed to v_mfma_i32_16x16x64_i8. gemm_i4_pp and gemm_i4_pp2 (K % 128 == 0,
+// the main path; gemm_i4_pp2 is its ping-pong form for 256-row tiles with
+// 16-bit outputs) stage packed words in LDS and widen after the LDS read; gemm_i4_mfma
 // (any K % 8 == 0) widens on the way from registers into LDS. Widening trick: XOR with 0x8 turns the offset code
 // (q + 8) into q's 4-bit two's-complement pattern; placing it in the high half
 // of a byte gives the int8 value 16*q. Both operands carry the factor 16, so the
@@ -414,7 +415,7 @@ __device__ inline uint32_t out_bits(typename OT::T v) {
 // added as in store_c_lds) written as 8-byte runs into an LDS tile; c_tile
 // points at the wave's first row and column, pitch in bytes.
 template <int FM, int WN, bool IL, class OT>
-__device__ inline void stage_c(const v4i (&acc)[FM][WN / 16], const float* ssa, const float* ssb, const float* sbias,
+__device__ __attribute__((always_inline)) inline void stage_c(const v4i (&acc)[FM][WN / 16], const float* ssa, const float* ssb, const float* sbias,
                                unsigned char* c_tile, int pitch, int li, int lg) {
   using T = typename OT::T;
   using CP = ColPlan<WN, IL>;
@@ -445,7 +446,7 @@ __device__ inline void stage_c(const v4i (&acc)[FM][WN / 16], const float* ssa, 
 // row (rows and columns past the matrix edge are skipped; C rows that are not
 // 16-byte aligned take element stores).
 template <int BM, int BN, int THREADS, class OT>
-__device__ inline void copy_out_c(const unsigned char* c_tile, int pitch, typename OT::T* out, int64_t ldc, int M,
+__device__ __attribute__((always_inline)) inline void copy_out_c(const unsigned char* c_tile, int pitch, typename OT::T* out, int64_t ldc, int M,
                                   int N, int m0, int n0, int tid) {
   using T = typename OT::T;
   constexpr int PPR = BN * 2 / 16;   // 16-byte pieces per row
@@ -694,6 +695,228 @@ gemm_i4_pp(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict
     store_c_lds<FM, WN, !B_NK, OT>(acc, s_sa + wm * WM, s_sb + wn * WN, sbias, out, ldc, M, N, m0 + wm * WM,
                                    n0 + wn * WN, li, lg);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong tiled kernel (gemm_i4_pp2): gemm_i4_pp's tile, stage ring and
+// operand layouts with the eight waves split into two groups of one wave per
+// SIMD (waves 0-3: rows 0 .. BM/2 - 1, waves 4-7: the rest) that alternate,
+// one slot apart, between a load slot (the stage's LDS reads, the copies of
+// stage t + 3, the widening of the stage's first half) and a compute slot (its
+// MFMAs, the second half widened in their shadow), with a workgroup barrier
+// between slots: on every SIMD one wave multiplies while the other loads.
+// The tile's scales are requested as raw bits before the first copies and
+// converted in the last load slot, where no copy is in flight any more. Each
+// group stages and copies out its half of the output tile while the other
+// group is still busy: group 0 stages its rows during group 1's last compute
+// slot.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, bool B_NK, class OT>
+__global__ void __launch_bounds__(512, 1)
+gemm_i4_pp2(const int32_t* __restrict__ a, int64_t lda, const int32_t* __restrict__ b, int64_t ldb,
+            const void* __restrict__ sa, int sad, const void* __restrict__ sb, int sbd,
+            typename OT::T* __restrict__ out, int64_t ldc, const typename OT::T* __restrict__ bias, int M, int N,
+            int K, int tiles_m) {
+  constexpr int WGM = 4, WGN = 2, W = 8, STAGES = 4;
+  using S = DmaStage<BM, BN, B_NK>;
+  using T = typename OT::T;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int FM = WM / 16, FN = WN / 16;
+  constexpr int PER = (S::DMA + W - 1) / W;
+  static_assert(BM == 256 && FM == 4 && WN % 16 == 0 && BN <= 256, "256-row tiles, 4 x 2 waves");
+  static_assert(sizeof(T) == 2, "16-bit outputs (staged epilogue)");
+  static_assert(S::A_DMA % W == 0, "copies 0 .. A_DMA / W - 1 of every wave are A's");
+  constexpr int TA = S::A_DMA / W;
+  constexpr int C_PITCH = BN * 2 + 16;
+  constexpr int RING = STAGES * S::BYTES, CTILE = BM * C_PITCH;
+  __shared__ __align__(16) unsigned char ring[RING > CTILE ? RING : CTILE];
+  __shared__ __align__(16) float s_sa[BM];
+  __shared__ __align__(16) float s_sb[BN];
+  __shared__ __align__(16) float s_bias[BN];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int li = lane & 15, lg = lane >> 4;
+  const bool grp1 = __builtin_amdgcn_readfirstlane(wave) >= W / 2;
+
+  const int nblk = gridDim.x;
+  int pid = blockIdx.x;
+  if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
+  constexpr int GM = 4;
+  const int tiles_n = (N + BN - 1) / BN;
+  const int g = pid / (GM * tiles_n), w = pid % (GM * tiles_n);
+  const int gm = min(GM, tiles_m - g * GM);
+  const int tm = g * GM + w % gm, tn = w / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = K >> 7;
+
+  const char* const a_base = reinterpret_cast<const char*>(a + (int64_t)m0 * lda);
+  const char* const b_base = reinterpret_cast<const char*>(B_NK ? b + (int64_t)n0 * ldb : b + n0);
+  const int64_t b_adv = B_NK ? 64 : 64 * ldb;
+  uint32_t dst[PER], voff[PER];
+#pragma unroll
+  for (int t = 0; t < PER; ++t) {
+    int i = __builtin_amdgcn_readfirstlane(wave) + W * t;
+    i = i < S::DMA ? i : S::DMA - 1;
+    if (t < TA) {
+      voff[t] = (uint32_t)(min(16 * i + li, M - 1 - m0) * (int)lda * 4 + 16 * lg);
+      dst[t] = i * 1024;
+    } else if (B_NK) {
+      const int c = i - S::A_DMA;
+      voff[t] = (uint32_t)(min(16 * c + li, N - 1 - n0) * (int)ldb * 4 + 16 * lg);
+      dst[t] = S::A_BYTES + c * 1024;
+    } else {
+      const int p = i - S::A_DMA;
+      voff[t] = (uint32_t)(p * (int)ldb * 4 + 4 * min(4 * lane, N - 4 - n0));
+      dst[t] = S::A_BYTES + p * S::KN_ROW;
+    }
+    dst[t] = __builtin_amdgcn_readfirstlane(dst[t]);
+  }
+  auto issue = [&](int ks, auto bufc) {
+    constexpr uint32_t BUF = decltype(bufc)::value * S::BYTES;
+    const uint32_t base = lds_addr(ring) + BUF;
+    const char* ab = a_base + 64 * (int64_t)ks;
+    const char* bb = b_base + b_adv * ks;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) dma16_s(voff[t], t < TA ? ab : bb, base + dst[t]);
+  };
+
+  using CP = ColPlan<WN, !B_NK>;
+  constexpr int N4 = CP::G4 > 0 ? CP::G4 : 1, N1 = FN - CP::J1 > 0 ? FN - CP::J1 : 1;
+  v4i ar[FM], br[B_NK ? FN : 1];
+  v4i b4[4][N4];
+  v2i b2[4];
+  int b1[4][N1];
+  auto word = [&](int j, int t) -> int {
+    if constexpr (B_NK) return br[j][t];
+    else if (j < CP::J2) return b4[t][j / 4][j % 4];
+    else if (j < CP::J1) return b2[t][j - CP::J2];
+    else return b1[t][j - CP::J1];
+  };
+  auto load_regs = [&](auto bufc) {
+    const unsigned char* base = ring + decltype(bufc)::value * S::BYTES;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) ar[i] = *reinterpret_cast<const v4i*>(base + (wm * FM + i) * 1024 + 16 * lane);
+    if constexpr (B_NK) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        br[j] = *reinterpret_cast<const v4i*>(base + S::A_BYTES + (wn * FN + j) * 1024 + 16 * lane);
+    } else {
+      const unsigned char* cols = base + S::A_BYTES + wn * WN * 4;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const unsigned char* row = cols + (4 * lg + t) * S::KN_ROW;
+#pragma unroll
+        for (int q = 0; q < CP::G4; ++q) b4[t][q] = *reinterpret_cast<const v4i*>(row + 256 * q + 16 * li);
+        if constexpr (CP::G2 > 0) b2[t] = *reinterpret_cast<const v2i*>(row + 256 * CP::G4 + 8 * li);
+#pragma unroll
+        for (int j = CP::J1; j < FN; ++j)
+          b1[t][j - CP::J1] =
+              *reinterpret_cast<const int*>(row + 256 * CP::G4 + 128 * CP::G2 + 64 * (j - CP::J1) + 4 * li);
+      }
+    }
+  };
+  auto wb = [&](int j, int h) -> v4i {
+    if constexpr (B_NK) return widen_pair64(br[j], h);
+    else return widen_pair(word(j, 2 * h), word(j, 2 * h + 1));
+  };
+  auto bar = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  v4i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  // The tile's scales and bias as raw bits, requested by group 0 before the
+  // first copies and converted in the last load slot (where the compiler's
+  // wait for them costs nothing: no copy is in flight there).
+  auto raw16 = [](const void* p, int64_t i) -> uint32_t { return reinterpret_cast<const uint16_t*>(p)[i]; };
+  auto raw32 = [](const void* p, int64_t i) -> uint32_t { return reinterpret_cast<const uint32_t*>(p)[i]; };
+  uint32_t rsa = 0, rsb = 0, rbias = 0;
+  if (tid < BM) {
+    const int64_t i = min(m0 + tid, M - 1);
+    rsa = sad == QO_DTYPE_F32 ? raw32(sa, i) : raw16(sa, i);
+    if (tid < BN) {
+      const int64_t j = min(n0 + tid, N - 1);
+      rsb = sbd == QO_DTYPE_F32 ? raw32(sb, j) : raw16(sb, j);
+      if (bias) rbias = raw16(bias, j);
+    }
+  }
+  issue(0, std::integral_constant<int, 0>{});
+  issue(min(1, nk - 1), std::integral_constant<int, 1>{});
+  issue(min(2, nk - 1), std::integral_constant<int, 2>{});
+  gemm_wait_vmcnt<PER * 2>();
+  lds_barrier();
+
+  if (grp1) bar();
+  auto phase = [&](int t, auto bufc) {
+    constexpr int J = decltype(bufc)::value;
+    load_regs(bufc);
+    if (t + 3 < nk) issue(t + 3, std::integral_constant<int, (J + 3) & 3>{});
+    // wait for this wave's copies of stage t + 1 (min(2, nk - 2 - t) younger stages may stay in flight)
+    gemm_wait_groups<PER, 2>(nk - 2 - t);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    if (t == nk - 1 && !grp1) {
+      asm volatile("" : "+v"(rsa), "+v"(rsb), "+v"(rbias));
+      if (tid < BM) s_sa[tid] = scale_from_bits(rsa, sad);
+      if (tid < BN) {
+        s_sb[tid] = scale_from_bits(rsb, sbd);
+        s_bias[tid] = (float)__builtin_bit_cast(T, (uint16_t)rbias);
+      }
+    }
+    // stage t's first half widened here; the second half one fragment ahead of its MFMAs
+    v4i fa[FM], fbn = wb(0, 0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[i] = widen_pair64(ar[i], 0);
+    bar();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const v4i fb = fbn;
+        if (j + 1 < FN) fbn = wb(j + 1, h);
+        else if (h == 0) fbn = wb(0, 1);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, fa[i], acc[i][j], 0, 0, 0);
+          if (h == 0 && j == FN - 1) fa[i] = widen_pair64(ar[i], 1);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 2 * FM * FN; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+    }
+    bar();
+  };
+  for (int s = 0; s < nk; s += 4) {
+    phase(s, std::integral_constant<int, 0>{});
+    if (s + 1 < nk) phase(s + 1, std::integral_constant<int, 1>{});
+    if (s + 2 < nk) phase(s + 2, std::integral_constant<int, 2>{});
+    if (s + 3 < nk) phase(s + 3, std::integral_constant<int, 3>{});
+  }
+  // Epilogue. Group 0 (rows 0 .. 127): stage its rows while group 1 runs its
+  // last compute slot, then copy them out while group 1 stages its rows;
+  // group 1 copies its rows out last.
+  const float* sbias = bias ? s_bias + wn * WN : nullptr;
+  unsigned char* const c_half = ring + (grp1 ? (BM / 2) * C_PITCH : 0);
+  auto stage_half = [&]() {
+    stage_c<FM, WN, !B_NK, OT>(acc, s_sa + wm * WM, s_sb + wn * WN, sbias, ring + wm * WM * C_PITCH + wn * WN * 2,
+                               C_PITCH, li, lg);
+  };
+  auto copy_half = [&]() {
+    copy_out_c<BM / 2, BN, 256, OT>(c_half, C_PITCH, out, ldc, M, N, m0 + (grp1 ? BM / 2 : 0), n0, tid & 255);
+  };
+  stage_half();
+  lds_barrier();
+  copy_half();
+  if (!grp1) bar();
 }
 
 // The epilogue of a skinny-kernel lane (row m, columns nc .. nc + 3). Its
@@ -1082,6 +1305,25 @@ static void launch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_t 
                      reinterpret_cast<const typename OT::T*>(bias), M, N, K, tiles_m);
 }
 
+// 256-row tiles: the ping-pong kernel for 16-bit outputs (its epilogue stages
+// 16-bit values), gemm_i4_pp for float32 outputs. Measured against gemm_i4_pp
+// (same process, outputs bit-equal): config 4 (4096 x 14336 x 4096, [K/8, N])
+// 200.7 -> 192.2 us, its W.t() layout 201.2 -> 187.8 us, 4096 x 4096 x 14336
+// W.t() bf16 (the linear layer at 4096 tokens) 172.8 -> 154.1 us.
+template <int BN, bool B_NK, class OT>
+static void launch_tiled(const int32_t* a, int64_t lda, const int32_t* b, int64_t ldb, const void* sa, int sad,
+                         const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int M, int N, int K,
+                         hipStream_t stream) {
+  if constexpr (sizeof(typename OT::T) == 2) {
+    const int tiles_m = (M + 255) / 256, tiles_n = (N + BN - 1) / BN;
+    launch((gemm_i4_pp2<256, BN, B_NK, OT>), dim3(tiles_m * tiles_n), dim3(512), 0, stream, a, lda, b, ldb, sa, sad,
+           sb, sbd, reinterpret_cast<typename OT::T*>(out), ldc, reinterpret_cast<const typename OT::T*>(bias), M, N, K,
+           tiles_m);
+  } else {
+    launch_dma<256, BN, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
+  }
+}
+
 // Fraction of the machine's workgroup slots doing useful output in a launch
 // of BM x BN tiles (one workgroup per CU): tile-count rounding plus ragged
 // edge tiles.
@@ -1105,9 +1347,9 @@ static void dispatch_dma(const int32_t* a, int64_t lda, const int32_t* b, int64_
   if (std::max(e224, e256) <= 0.5)
     launch_dma<128, 128, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
   else if (e224 > e256)
-    launch_dma<256, 224, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
+    launch_tiled<224, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
   else
-    launch_dma<256, 256, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
+    launch_tiled<256, B_NK, OT>(a, lda, b, ldb, sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
 }
 
 // QO_ROUTE_GEMM_NO_SKINNY sends small M to the tiled kernels (tests use it to

@@ -1,0 +1,87 @@
+// Microbenchmarks of the hardware ceilings the design is measured against
+// (measurement infrastructure for bench.py --ceilings; not part of the C ABI):
+//
+//  * qo_probe_mfma_i8: v_mfma_i32_16x16x64_i8 issue rate with a chosen number
+//    of independent VALU instructions per MFMA, one or two waves per SIMD on
+//    every CU (the int8 matrix-core ceiling under load, and how much VALU work
+//    it hides);
+//  * qo_probe_empty: an empty kernel (launch and wave start-up cost);
+//  * qo_probe_stream: a streaming kernel with the quantize's traffic shape,
+//    16 bytes read and 4 bytes written per lane per step (config 2 reads
+//    16.8 MB of fp16 activations and writes 4.2 MB of packed codes).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// KV independent VALU instructions (one v_xor each, on four rotating
+// registers) after each MFMA; eight independent accumulator chains.
+template <int KV>
+__global__ void __launch_bounds__(512) probe_mfma_i8(int iters, int* out) {
+  const int t = threadIdx.x;
+  const v4i a = {t, 1, 2, 3}, b = {3, 2, 1, t};
+  v4i acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = v4i{0, 0, 0, 0};
+  uint32_t x0 = t, x1 = 3 * t, x2 = 5 * t, x3 = 7 * t;
+  const uint32_t c = 0x5bd1e995u;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+      for (int k = 0; k < KV; ++k) {
+        if (k % 4 == 0) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x0) : "v"(c));
+        if (k % 4 == 1) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x1) : "v"(c));
+        if (k % 4 == 2) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x2) : "v"(c));
+        if (k % 4 == 3) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x3) : "v"(c));
+      }
+    }
+  }
+  int s = (int)(x0 ^ x1 ^ x2 ^ x3);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  out[blockIdx.x * blockDim.x + t] = s;
+}
+
+__global__ void probe_empty() {}
+
+// grid-stride: 16 bytes in, their four words XORed into 4 bytes out
+__global__ void __launch_bounds__(256) probe_stream(const v4i* __restrict__ in, int* __restrict__ out, int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x) {
+    const v4i v = in[i];
+    out[i] = v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+}
+
+}  // namespace
+
+// threads per block: 512 (two waves per SIMD) or 256 (one)
+extern "C" int qo_probe_mfma_i8(int kvalu, int blocks, int iters, int* out, void* stream, int threads) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (threads != 256 && threads != 512) return 1;
+  switch (kvalu) {
+    case 0: probe_mfma_i8<0><<<blocks, threads, 0, s>>>(iters, out); break;
+    case 1: probe_mfma_i8<1><<<blocks, threads, 0, s>>>(iters, out); break;
+    case 2: probe_mfma_i8<2><<<blocks, threads, 0, s>>>(iters, out); break;
+    case 3: probe_mfma_i8<3><<<blocks, threads, 0, s>>>(iters, out); break;
+    case 4: probe_mfma_i8<4><<<blocks, threads, 0, s>>>(iters, out); break;
+    case 8: probe_mfma_i8<8><<<blocks, threads, 0, s>>>(iters, out); break;
+    default: return 1;
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int qo_probe_empty(void* stream) {
+  probe_empty<<<1, 64, 0, reinterpret_cast<hipStream_t>(stream)>>>();
+  return (int)hipGetLastError();
+}
+
+extern "C" int qo_probe_stream(const void* in, void* out, int64_t bytes_in, int blocks, void* stream) {
+  if (bytes_in % 16 != 0) return 1;
+  probe_stream<<<blocks, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(static_cast<const v4i*>(in),
+                                                                         static_cast<int*>(out), bytes_in / 16);
+  return (int)hipGetLastError();
+}
