@@ -36,6 +36,7 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--warm-s 0.2] [--no
        python bench.py --pmc-summary FETCH_DIR WRITE_DIR
        python bench.py --pmc-table PMC_DIR [PMC_DIR ...]
        python bench.py --ceilings                       (int8 MFMA rate, empty launch, streaming copy)
+       python bench.py --ceilings-summary KERNEL_TRACE_CSV
        python bench.py --trace-summary KERNEL_TRACE_CSV [--trace-last K]
                                                         (rocprofv3 --kernel-trace --output-format csv)
 """
@@ -476,11 +477,11 @@ def cpu_dequant(torch, budget_s):
 
 # Kernel of each benched workload, as rocprofv3 names it (a substring of the demangled name).
 KERNEL_OF = {
-    "gemm_cfg4": "gemm_i4_pp<256, 224, 4, 2, 4, false, qo::OutF16>",
+    "gemm_cfg4": "gemm_i4_pp2<256, 224, false, qo::OutF16>",
     "quantize_cfg2": "fq_wave_kernel<qo::F16T, 4, 2, true>",
     "quantize_cfg3": "fq_few2_kernel<qo::BF16T, 7, true>",
     "gemm_cfg5_T16": "gemm_i4_skinny_nk",
-    "gemm_cfg5_T4096": "gemm_i4_pp<256, 256, 4, 2, 4, true, qo::OutBF16>",
+    "gemm_cfg5_T4096": "gemm_i4_pp2<256, 256, true, qo::OutBF16>",
 }
 COPY_PROBE_BYTES = 1 << 30      # float32 negation of 1 GiB: reads and writes exactly this many bytes
 COPY_PROBE_KERNEL = "neg_kernel"
@@ -635,6 +636,34 @@ BENCH_SEGMENTS = [
 ]
 
 
+def ceilings_summary(trace_csv):
+    """Per-probe kernel durations from a rocprofv3 --kernel-trace CSV of
+    ``bench.py --ceilings`` (the MFMA probe split by workgroup size: 512
+    threads = two waves per SIMD, 256 = one)."""
+    import csv
+    from collections import defaultdict
+
+    groups = defaultdict(list)
+    for r in csv.DictReader(open(trace_csv)):
+        name = r["Kernel_Name"]
+        if "probe_" not in name:
+            continue
+        short = name.split("(anonymous namespace)::", 1)[-1].split("(")[0]
+        groups[(short, int(r["Workgroup_Size_X"]), int(r["Grid_Size_X"]))].append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print(f"{'probe':28s} {'block':>5s} {'grid':>9s} {'calls':>6s} {'avg_us':>9s} {'median_us':>9s}  rate")
+    for (short, block, grid), v in sorted(groups.items(), key=lambda kv: (kv[0][0], -kv[0][1])):
+        v.sort()
+        avg, med = sum(v) / len(v), v[len(v) // 2]
+        rate = ""
+        if short.startswith("probe_mfma_i8"):
+            waves = grid // 64
+            rate = f"{2 * 16 * 16 * 64 * 8 * 4096 * waves / (med * 1e-6) / 1e12:.0f} TOP/s (median)"
+        elif short.startswith("probe_stream"):
+            rate = f"{2048 * 4096 * 2 * 5 / 4 / (med * 1e-6) / 1e9:.0f} GB/s (median)"
+        print(f"{short:28s} {block:5d} {grid:9d} {len(v):6d} {avg:9.2f} {med:9.2f}  {rate}")
+
+
 def trace_summary(trace_csv, tail=None):
     """Per-workload kernel durations from a rocprofv3 --kernel-trace CSV of a default bench run.
 
@@ -774,6 +803,8 @@ def main():
                     help="per-kernel medians of every counter in rocprofv3 --pmc output folders of --pmc-pass")
     ap.add_argument("--ceilings", action="store_true",
                     help="microbenchmarks of the int8 MFMA rate, an empty launch and a streaming copy")
+    ap.add_argument("--ceilings-summary", metavar="KERNEL_TRACE_CSV",
+                    help="per-probe kernel durations from a rocprofv3 kernel trace of --ceilings")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
@@ -783,6 +814,9 @@ def main():
         return
     if args.trace_summary:
         trace_summary(args.trace_summary, args.trace_last)
+        return
+    if args.ceilings_summary:
+        ceilings_summary(args.ceilings_summary)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the hot path shards over tokens with no "
