@@ -388,6 +388,35 @@ def test_quantize_strided_rows_and_empty(gpu):
     assert q.shape == (0, 512) and s.shape == (0,)
 
 
+@pytest.mark.parametrize("m", [112, 96])
+@pytest.mark.parametrize("tokens", [16, 600])
+def test_few_token_kernels_padded_rows(gpu, m, tokens):
+    """X rows at a stride above their length (a slice of a wider activation
+    buffer: x_ld = F + 64) through the N = 128 kernels (112 x 128 on the
+    two-slot few-token kernel, 96 x 128 on the few-token kernel), for the
+    quantize alone and through the linear layer: bit for bit the results of
+    the contiguous rows."""
+    n, f, out_f = 128, m * 128, 1024
+    x = wl.activations(tokens, f, torch.bfloat16, seed=tokens + m, outlier_frac=0.005, outlier_scale=30.0)
+    L, R = wl.orthogonal(m, 71, torch.bfloat16).to(gpu), wl.orthogonal(n, 72, torch.bfloat16).to(gpu)
+    wide = torch.zeros(tokens, f + 64, dtype=torch.bfloat16)
+    wide[:, :f] = x
+    xs = wide.to(gpu)[:, :f]
+    xc = x.to(gpu)
+    assert xs.stride(0) == f + 64 and not xs.is_contiguous()
+    _say(f"padded rows {tokens} x {m}x{n}")
+    q1, s1 = capi.flatquant_quantize(xs, L, R, 0.9, True)
+    q2, s2 = capi.flatquant_quantize(xc, L, R, 0.9, True)
+    w = wl.random_packed(out_f, f // 8, 73).to(gpu)
+    sw = wl.uniform(out_f, 0.001, 0.01, 74).to(gpu)
+    y1, qa, sa1 = capi.w4a4_linear(xs, L, R, w, sw, 0.9)
+    y2, qb, sb2 = capi.w4a4_linear(xc, L, R, w, sw, 0.9)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+    assert torch.equal(qa, q2) and torch.equal(sa1, s2) and torch.equal(y1, y2) and torch.equal(qb, q2)
+    check_quant(x, L.cpu(), R.cpu(), 0.9, True, q1, s1, f"padded rows {tokens} x {m}x{n}")
+
+
 def test_quantize_torch_op_matches_capi_and_stream(gpu):
     case = wl.quant_cfg2(tokens=300, seed=3)
     x, L, R = case.x.to(gpu), case.left.to(gpu), case.right.to(gpu)
