@@ -541,6 +541,27 @@ struct FqEpi<BF16T> {
     return ev | (od << 4);
   }
 
+  // word_u8 for a token whose largest quotient rounds below 7.5 (every code
+  // then lies in -8 .. 7 without the upper clamp; the lower one is the u8
+  // conversion's saturation at 0 either way): each quotient is rounded to
+  // bf16 straight into a float32 register by one v_cvt_pk_bf16_f32 whose low
+  // half is the conversion of 0.0 (the bf16 value's float32 bits, low half
+  // zero), so no unpacking of a rounded pair is needed: 10 VALU per pair of
+  // codes instead of 12.
+  __device__ static inline uint32_t word_u8_noclamp(const uint32_t (&p)[4], float rcp) {
+    uint32_t ev = 0u, od = 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float t0, t1;   // operands are VALU products, never MFMA results
+      asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(t0) : "v"(lo(p[r]) * rcp));
+      asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(t1) : "v"(hi(p[r]) * rcp));
+      uint32_t& d = (r & 1) ? od : ev;
+      d = __builtin_amdgcn_cvt_pk_u8_f32(t0 + 8.0f, r >> 1, d);
+      d = __builtin_amdgcn_cvt_pk_u8_f32(t1 + 8.0f, 2 + (r >> 1), d);
+    }
+    return ev | (od << 4);
+  }
+
   // max |y| of rounded Y pairs as a 16-bit pattern (sign-cleared bf16 bits
   // order like the values).
   struct Amax {
@@ -1147,14 +1168,17 @@ __device__ inline float few_scale(float amax, float* red, int q, int lane, float
 // rcp = 1 / s, without branches or divisions (either would end the block the
 // products are scheduled with): a scale of 0 (an all-zero fp16 token) stores
 // wrong words here, which few_codes_zero_scale then replaces.
-template <class DT, int MB>
+// NOCLAMP (bf16): the token's largest quotient rounds below 7.5 (see
+// FqEpi<BF16T>::word_u8_noclamp).
+template <class DT, int MB, bool NOCLAMP = false>
 __device__ inline void few_codes_packed(const uint32_t (&yp)[MB][4], float rcp, int32_t* orow, int li) {
   using Epi = FqEpi<DT>;
   constexpr int N = FewShape<MB>::N;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     uint32_t w;
-    if constexpr (std::is_same<DT, BF16T>::value) w = Epi::word_u8(yp[mb], rcp);
+    if constexpr (std::is_same<DT, BF16T>::value && NOCLAMP) w = Epi::word_u8_noclamp(yp[mb], rcp);
+    else if constexpr (std::is_same<DT, BF16T>::value) w = Epi::word_u8(yp[mb], rcp);
     else w = Epi::template word4<true>(yp[mb], rcp);   // the lower clamp as well: valid for any amax
     orow[(16 * mb + li) * (N / 8)] = (int32_t)w;
   }
@@ -1471,7 +1495,7 @@ struct FewLdsCompact {
   static_assert(STAGE_OFF % 16 == 0 && BYTES <= 80 * 1024, "two workgroups per CU");
 };
 
-template <class DT, int MB, bool PACK>
+template <class DT, int MB, bool PACK, bool NOCLAMP>
 __device__ __attribute__((always_inline)) inline void few_quantize_compact(
     unsigned char* lds, const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
     const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
@@ -1583,7 +1607,7 @@ __device__ __attribute__((always_inline)) inline void few_quantize_compact(
     if (q == 0 && lane == 0) out_scales[t] = sc;
     if constexpr (PACK) {
       int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (S::F / 8) + 4 * q + lg;
-      few_codes_packed<DT, MB>(yp, 1.0f / sc, orow, li);
+      few_codes_packed<DT, MB, NOCLAMP>(yp, 1.0f / sc, orow, li);
       if (!(sc > 0.f)) few_codes_zero_scale<DT, MB>(yp, sc, orow, li);
     } else {
       few_codes_int8<DT, MB>(yp, sc, reinterpret_cast<int8_t*>(out_codes) + t * S::F + 32 * q + 8 * lg, li);
@@ -1638,7 +1662,9 @@ __device__ inline void read_ahead_rows(const v4i* __restrict__ p, int64_t rows, 
 }
 
 // Workgroups 0 .. qgroups - 1 quantize; the rest, if any, read ahead.
-template <class DT, int MB, bool PACK>
+// NOCLAMP (bf16, packed codes): the host has found from the clip ratio that no
+// quotient can round to 7.5 or above (kNoClampClip).
+template <class DT, int MB, bool PACK, bool NOCLAMP = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fq_few2_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
                const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
@@ -1649,8 +1675,8 @@ fq_few2_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
     read_ahead_rows(ahead, ahead_rows, ahead_rs16, ahead_len16, qgroups);
     return;
   }
-  few_quantize_compact<DT, MB, PACK>(lds, x, tokens, x_ld, left, right, clip, out_codes, out_scales, blockIdx.x,
-                                     qgroups);
+  few_quantize_compact<DT, MB, PACK, NOCLAMP>(lds, x, tokens, x_ld, left, right, clip, out_codes, out_scales,
+                                              blockIdx.x, qgroups);
 }
 
 // ---------------------------------------------------------------------------
@@ -2352,6 +2378,16 @@ static int launch_wave(const void* x, int64_t tokens, int64_t x_ld, const void* 
 // * 128 x 128 stays on one slot (its compact form spills).
 constexpr int64_t kFewTwoSlots = 2;
 
+// bf16 codes need no upper clamp when clip >= kNoClampClip. With c the clip
+// ratio and every rounding's relative error bounded (2^-8 for bf16, 2^-24 for
+// float32): bound = rnd(amax c) >= amax c (1 - 2^-24)(1 - 2^-8), s = rnd(bound
+// / 7) >= bound / 7 (1 - 2^-24)(1 - 2^-8), rcp <= (1 + 2^-24) / s, so the
+// largest quotient u = fl(amax rcp) <= 7 (1 + 2^-24)^2 / (c (1 - 2^-24)^2
+// (1 - 2^-8)^2), which is below 7.484375 (the least float32 that rounds to
+// bf16 7.5 or above) for c > 0.9427. The clamp of the scale at rnd(1e-8)
+// only makes s larger.
+constexpr float kNoClampClip = 0.95f;
+
 template <class DT, int MB, bool PACK>
 static int launch_few(const void* x, int64_t tokens, int64_t x_ld, const void* left, const void* right, float clip,
                       void* out_codes, float* out_scales, hipStream_t stream, const ReadAhead& ra) {
@@ -2374,11 +2410,19 @@ static int launch_few(const void* x, int64_t tokens, int64_t x_ld, const void* l
     const bool ahead = ra.p && ra.rows > 0 && ra.row_len >= 16 && (uintptr_t)ra.p % 16 == 0 &&
                        ra.row_bytes % 16 == 0 && ra.row_len % 16 == 0 && ra.row_len <= ra.row_bytes &&
                        (ra.rows + 256) * (ra.row_len / 16) < INT32_MAX / 2 && grid < 2 * cus;
-    launch((fq_few2_kernel<DT, MB, PACK>), dim3((unsigned)(ahead ? 2 * cus : grid)), dim3(256), 0, stream,
-           reinterpret_cast<const T*>(x), tokens, x_ld, reinterpret_cast<const T*>(left),
-           reinterpret_cast<const T*>(right), clip, out_codes, out_scales, (int)grid,
-           reinterpret_cast<const v4i*>(ra.p), ahead ? ra.rows : (int64_t)0, ra.row_bytes / 16,
-           ahead ? (int)(ra.row_len / 16) : 0);
+    auto go = [&](auto kernel) {
+      launch(kernel, dim3((unsigned)(ahead ? 2 * cus : grid)), dim3(256), 0, stream, reinterpret_cast<const T*>(x),
+             tokens, x_ld, reinterpret_cast<const T*>(left), reinterpret_cast<const T*>(right), clip, out_codes,
+             out_scales, (int)grid, reinterpret_cast<const v4i*>(ra.p), ahead ? ra.rows : (int64_t)0,
+             ra.row_bytes / 16, ahead ? (int)(ra.row_len / 16) : 0);
+    };
+    if constexpr (std::is_same<DT, BF16T>::value && PACK) {
+      if (clip >= kNoClampClip) {
+        go(fq_few2_kernel<DT, MB, PACK, true>);
+        return QO_OK;
+      }
+    }
+    go(fq_few2_kernel<DT, MB, PACK>);
     return QO_OK;
   }
   // one token at a time per workgroup (four waves, one per SIMD); workgroups loop beyond one per CU

@@ -284,6 +284,28 @@ def test_quantize_few_token_kernel_matches_pair_kernel(gpu, tokens, m, dtype, pa
         check_quant(case.x, case.left, case.right, 0.9, pack, q1, s1, f"few-token {m}x128 {dtype}")
 
 
+@pytest.mark.parametrize("m", [112, 64])
+@pytest.mark.parametrize("clip", [1.0, 0.97, 0.95, 0.9499, 0.94])
+def test_quantize_few2_bf16_codes_at_clip_boundary(gpu, m, clip, routing):
+    """bf16 packed codes of fq_few2_kernel skip the upper clamp when clip >=
+    0.95 (no quotient can then round to 7.5); below that they clamp. Both
+    forms equal the pair kernel bit for bit on either side of the boundary,
+    with tokens whose values cluster near max |Y| (many codes of +-7)."""
+    case = wl.quant_case("clip", 600, m, 128, torch.bfloat16, clip, True, seed=int(clip * 1e4) + m,
+                         outlier_frac=0.005, outlier_scale=30.0)
+    g = torch.Generator().manual_seed(5)
+    y = torch.sign(torch.randn(64, m, 128, generator=g)) * (1.0 + 0.01 * torch.rand(64, m, 128, generator=g))
+    L, R = case.left.float(), case.right.float()
+    case.x[:64] = (L @ y @ R.T).reshape(64, m * 128).to(torch.bfloat16)   # Y = L^T X R is about y
+    _say(f"few2 bf16 codes at clip {clip} {m}x128")
+    q1, s1 = run_capi_quant(case, gpu)
+    routing.on("FQ_NO_FEW")
+    q2, s2 = run_capi_quant(case, gpu)
+    routing.off("FQ_NO_FEW")
+    assert torch.equal(s1, s2) and torch.equal(q1, q2)
+    check_quant(case.x, case.left, case.right, clip, True, q1, s1, f"few2 clip {clip}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mn", [(64, 64), (112, 128), (16, 16)])
 def test_quantize_matches_sequential_accumulation_oracle(gpu, dtype, mn, routing):
