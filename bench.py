@@ -36,6 +36,7 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--warm-s 0.2] [--no
        python bench.py --pmc-summary FETCH_DIR WRITE_DIR
        python bench.py --pmc-table PMC_DIR [PMC_DIR ...]
        python bench.py --ceilings                       (int8 MFMA rate, empty launch, streaming copy)
+       python bench.py --power                          (board power and clock while each kernel loops)
        python bench.py --ceilings-summary KERNEL_TRACE_CSV
        python bench.py --trace-summary KERNEL_TRACE_CSV [--trace-last K]
                                                         (rocprofv3 --kernel-trace --output-format csv)
@@ -657,7 +658,7 @@ def ceilings_summary(trace_csv):
         avg, med = sum(v) / len(v), v[len(v) // 2]
         rate = ""
         if short.startswith("probe_mfma_i8"):
-            waves = grid // 64
+            waves = grid // 64   # the data probe's rows mix its zero and random runs; bench.py's log splits them
             rate = f"{2 * 16 * 16 * 64 * 8 * 4096 * waves / (med * 1e-6) / 1e12:.0f} TOP/s (median)"
         elif short.startswith("probe_stream"):
             rate = f"{2048 * 4096 * 2 * 5 / 4 / (med * 1e-6) / 1e9:.0f} GB/s (median)"
@@ -755,6 +756,30 @@ def ceilings(torch, steps, warmup, dev):
                  f"{mfma[f'valu_per_mfma_{kv}']['TOPS']:.0f} TOP/s")
         out[key] = mfma
 
+    # operands from memory: all-zero bytes, random bytes, random bytes with the
+    # low nibble cleared (the GEMM's widened int4 codes, 16 q), and random bytes
+    # with the high nibble cleared (offset codes q + 8 in 0 .. 15)
+    lib.qo_probe_mfma_i8_data.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_int]
+    cycles = torch.empty(cus * 8, dtype=torch.int64, device=dev)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    rnd = torch.randint(-2**31, 2**31 - 1, (16 * 1024 * 4,), generator=g, dtype=torch.int64).to(torch.int32)
+    srcs = {"zero": torch.zeros_like(rnd).to(dev), "random": rnd.to(dev),
+            "widened_int4": (rnd & int(0xF0F0F0F0 - 2**32)).to(dev), "low_nibble": (rnd & 0x0F0F0F0F).to(dev)}
+    data = {}
+    for name, src in srcs.items():
+        for kv in (0, 2, 4):
+            def launch(i, kv=kv, src=src):
+                assert lib.qo_probe_mfma_i8_data(kv, cus, iters, ctypes.c_void_p(src.data_ptr()),
+                                                 ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(cycles.data_ptr()),
+                                                 stream(), 512) == 0
+            ms, _ = _time_graph(torch, launch, steps, warmup)
+            us = ms / steps * 1e3
+            ops = 2 * 16 * 16 * 64 * 8 * iters * 8 * cus
+            data[f"{name}_valu_per_mfma_{kv}"] = {"us_per_launch": us, "TOPS": ops / (us * 1e-6) / 1e12}
+            _log(f"ceiling: int8 MFMA on {name} operands, two waves per SIMD, {kv} VALU per MFMA: "
+                 f"{ops / (us * 1e-6) / 1e12:.0f} TOP/s")
+    out["mfma_i8_operands_from_memory"] = data
+
     def launch_empty(i):
         assert lib.qo_probe_empty(stream()) == 0
     ms, _ = _time_graph(torch, launch_empty, steps, warmup)
@@ -777,6 +802,92 @@ def ceilings(torch, steps, warmup, dev):
         _log(f"ceiling: stream of config 2's bytes, {blocks} blocks: {us:.2f} us")
     out["stream_cfg2_bytes"] = stream_res
     print(json.dumps({"ceilings": out}), flush=True)
+
+
+def _smi_sample():
+    """(board power W, shader clock MHz) read by amd-smi and rocm-smi (child processes); None where absent."""
+    import re
+    import subprocess
+
+    def run(cmd):
+        try:
+            return subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                                  timeout=20).stdout
+        except (OSError, subprocess.SubprocessError):
+            return ""
+    pw = re.search(r"SOCKET_POWER:\s*([\d.]+)\s*W", run(["amd-smi", "metric", "-p"]))
+    clk = re.search(r"sclk clock level:\s*\d+:\s*\((\d+)\s*Mhz\)", run(["rocm-smi", "--showclocks"]), re.I)
+    return (float(pw.group(1)) if pw else None), (float(clk.group(1)) if clk else None)
+
+
+def power(torch, dev, seconds=2.0):
+    """Board power and shader clock while each workload runs back to back:
+    the MFMA probe on zero, widened-int4 and random operands, the config 4 and
+    config 5 (T = 4096) GEMMs and the config 2 and config 3 quantizes. Each
+    runs in a loop on a thread for ``seconds`` before three samples are taken
+    (medians reported); one JSON line."""
+    import ctypes
+    import statistics
+    import threading
+    from quant_ops_amd import capi
+    from quant_ops_amd import workloads as wl
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "quant_ops_amd", "libquant_ops_probes.so"))
+    c_vp, c_int = ctypes.c_void_p, ctypes.c_int
+    lib.qo_probe_mfma_i8_data.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_int]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(cus * 512, dtype=torch.int32, device=dev)
+    cycles = torch.empty(cus * 8, dtype=torch.int64, device=dev)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    rnd = torch.randint(-2**31, 2**31 - 1, (16 * 1024 * 4,), generator=g, dtype=torch.int64).to(torch.int32)
+    srcs = {"zero": torch.zeros_like(rnd).to(dev), "widened_int4": (rnd & int(0xF0F0F0F0 - 2**32)).to(dev),
+            "random": rnd.to(dev)}
+
+    def probe(src, kv):
+        return lambda: lib.qo_probe_mfma_i8_data(kv, cus, 16384, ctypes.c_void_p(src.data_ptr()),
+                                                 ctypes.c_void_p(sink.data_ptr()),
+                                                 ctypes.c_void_p(cycles.data_ptr()), None, 512)
+
+    def gemm(case):
+        a, b, sa, sb = case.a.to(dev), case.b.to(dev), case.scale_a.to(dev), case.scale_b.to(dev)
+        out = torch.empty(case.mnk[:2], dtype=case.out_dtype, device=dev)
+        return lambda: capi.int4_gemm(a, b, sa, sb, out_dtype=case.out_dtype, out=out)
+
+    def quant(case):
+        x, L, R = case.x.to(dev), case.left.to(dev), case.right.to(dev)
+        return lambda: capi.flatquant_quantize(x, L, R, case.clip_ratio, case.pack_int32)
+
+    work = [("idle", None)]
+    for name in srcs:
+        for kv in (0, 2):
+            work.append((f"mfma_i8 probe, {name} operands, {kv} VALU per MFMA", probe(srcs[name], kv)))
+    work += [("gemm cfg4", gemm(wl.gemm_cfg4())),
+             ("gemm cfg5 T=4096", gemm(wl.gemm_case(4096, 4096, 14336, seed=2, b_transposed_view=True,
+                                                    out_dtype=torch.bfloat16))),
+             ("quantize cfg3", quant(wl.quant_cfg3())), ("quantize cfg2", quant(wl.quant_cfg2()))]
+    out = {}
+    for name, fn in work:
+        stop = []
+
+        def loop():
+            while not stop:
+                for _ in range(20):
+                    fn()
+                torch.cuda.synchronize()
+        th = threading.Thread(target=loop) if fn else None
+        if th:
+            th.start()
+        time.sleep(seconds if th else 0.5)
+        samples = [_smi_sample() for _ in range(3)]
+        stop.append(True)
+        if th:
+            th.join()
+        pw = [p for p, _ in samples if p is not None]
+        ck = [c for _, c in samples if c is not None]
+        out[name] = {"power_W": statistics.median(pw) if pw else None,
+                     "sclk_MHz": statistics.median(ck) if ck else None}
+        _log(f"power: {name}: {out[name]['power_W']} W, {out[name]['sclk_MHz']} MHz")
+    print(json.dumps({"power": out}), flush=True)
 
 
 # --------------------------------------------------------------------------- main
@@ -803,6 +914,8 @@ def main():
                     help="per-kernel medians of every counter in rocprofv3 --pmc output folders of --pmc-pass")
     ap.add_argument("--ceilings", action="store_true",
                     help="microbenchmarks of the int8 MFMA rate, an empty launch and a streaming copy")
+    ap.add_argument("--power", action="store_true",
+                    help="board power and shader clock (amd-smi, rocm-smi) while each benched kernel loops")
     ap.add_argument("--ceilings-summary", metavar="KERNEL_TRACE_CSV",
                     help="per-probe kernel durations from a rocprofv3 kernel trace of --ceilings")
     args = ap.parse_args()
@@ -845,6 +958,9 @@ def main():
         return
     if args.ceilings:
         ceilings(torch, args.steps, args.warmup, dev)
+        return
+    if args.power:
+        power(torch, dev)
         return
     steps, warmup = args.steps, args.warmup
 

@@ -5,6 +5,10 @@
 //    of independent VALU instructions per MFMA, one or two waves per SIMD on
 //    every CU (the int8 matrix-core ceiling under load, and how much VALU work
 //    it hides);
+//  * qo_probe_mfma_i8_data: the same with operands taken from a buffer of
+//    random bytes (eight different A and B fragments per lane in turn, so the
+//    matrix cores switch like they do on real data; constant operands draw
+//    less power), and each wave's s_memtime ticks over the loop;
 //  * qo_probe_empty: an empty kernel (launch and wave start-up cost);
 //  * qo_probe_stream: a streaming kernel with the quantize's traffic shape,
 //    16 bytes read and 4 bytes written per lane per step (config 2 reads
@@ -46,6 +50,45 @@ __global__ void __launch_bounds__(512) probe_mfma_i8(int iters, int* out) {
   out[blockIdx.x * blockDim.x + t] = s;
 }
 
+// Operands from `src` (16 x 1024 fragments of 16 bytes; wave w of block b takes
+// set (8 b + w) % 16): eight (A, B) pairs per lane, MFMA j on pair j.
+// cycles[global wave] = s_memtime at the loop's end minus at its start.
+template <int KV>
+__global__ void __launch_bounds__(512) probe_mfma_i8_data(int iters, const v4i* __restrict__ src, int* out,
+                                                          unsigned long long* cycles) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const v4i* set = src + (size_t)((blockIdx.x * 8 + wave) % 16) * 1024;
+  v4i a[8], b[8], acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    a[j] = set[j * 64 + lane];
+    b[j] = set[512 + j * 64 + lane];
+    acc[j] = v4i{0, 0, 0, 0};
+  }
+  uint32_t x0 = t, x1 = 3 * t, x2 = 5 * t, x3 = 7 * t;
+  const uint32_t c = 0x5bd1e995u;
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[j], b[j], acc[j], 0, 0, 0);
+#pragma unroll
+      for (int k = 0; k < KV; ++k) {
+        if (k % 4 == 0) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x0) : "v"(c));
+        if (k % 4 == 1) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x1) : "v"(c));
+        if (k % 4 == 2) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x2) : "v"(c));
+        if (k % 4 == 3) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x3) : "v"(c));
+      }
+    }
+  }
+  int s = (int)(x0 ^ x1 ^ x2 ^ x3);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  out[blockIdx.x * blockDim.x + t] = s;
+  if (lane == 0) cycles[blockIdx.x * (blockDim.x >> 6) + wave] = t1 - t0;
+}
+
 __global__ void probe_empty() {}
 
 // grid-stride: 16 bytes in, their four words XORed into 4 bytes out
@@ -69,6 +112,21 @@ extern "C" int qo_probe_mfma_i8(int kvalu, int blocks, int iters, int* out, void
     case 3: probe_mfma_i8<3><<<blocks, threads, 0, s>>>(iters, out); break;
     case 4: probe_mfma_i8<4><<<blocks, threads, 0, s>>>(iters, out); break;
     case 8: probe_mfma_i8<8><<<blocks, threads, 0, s>>>(iters, out); break;
+    default: return 1;
+  }
+  return (int)hipGetLastError();
+}
+
+// src: 16 x 1024 x 16 bytes; out: blocks x threads ints; cycles: blocks x threads / 64
+extern "C" int qo_probe_mfma_i8_data(int kvalu, int blocks, int iters, const void* src, int* out,
+                                     unsigned long long* cycles, void* stream, int threads) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (threads != 256 && threads != 512) return 1;
+  const v4i* v = static_cast<const v4i*>(src);
+  switch (kvalu) {
+    case 0: probe_mfma_i8_data<0><<<blocks, threads, 0, s>>>(iters, v, out, cycles); break;
+    case 2: probe_mfma_i8_data<2><<<blocks, threads, 0, s>>>(iters, v, out, cycles); break;
+    case 4: probe_mfma_i8_data<4><<<blocks, threads, 0, s>>>(iters, v, out, cycles); break;
     default: return 1;
   }
   return (int)hipGetLastError();
