@@ -8,9 +8,10 @@ VMEM instruction reads that SGPR; the hardware does not interlock it, and the
 compiler inserts the wait states for the instructions it generates but not for
 inline assembly. A copy that read a stale base would address the wrong memory.
 
-This test disassembles ``libquant_ops_hip.so``'s gfx950 code object and fails
-if any LDS-DMA instruction reads an SGPR that a VALU instruction wrote fewer
-than five wait states before it.
+This test disassembles every gfx950 code object in ``libquant_ops_hip.so``
+(one offload bundle per source file, concatenated in the ``.hip_fatbin``
+section) and fails if any LDS-DMA instruction reads an SGPR that a VALU
+instruction wrote fewer than five wait states before it.
 """
 import os
 import re
@@ -74,23 +75,51 @@ def test_scanner_finds_the_pattern():
     assert scan_lds_dma_hazards(far) == []
 
 
-@pytest.mark.skipif(not os.path.exists(LIB), reason="library not built")
-@pytest.mark.skipif(not all(os.path.exists(os.path.join(LLVM, t)) for t in TOOLS), reason="ROCm LLVM tools absent")
-def test_no_valu_sgpr_hazard_before_lds_dma(tmp_path):
+BUNDLE_MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
+
+
+def gfx950_disassembly(lib, tmp_path):
+    """Disassembly text of every gfx950 code object in ``lib``'s .hip_fatbin
+    section (the section holds one offload bundle per source file)."""
     fatbin = tmp_path / "fatbin.bin"
-    co = tmp_path / "gfx950.co"
-    subprocess.run([os.path.join(LLVM, "llvm-objcopy"), f"--dump-section=.hip_fatbin={fatbin}", LIB,
+    subprocess.run([os.path.join(LLVM, "llvm-objcopy"), f"--dump-section=.hip_fatbin={fatbin}", lib,
                     str(tmp_path / "lib.copy")], check=True)
-    subprocess.run([os.path.join(LLVM, "clang-offload-bundler"), "--unbundle", "--type=o", f"--input={fatbin}",
-                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={co}"], check=True)
-    dis = subprocess.run([os.path.join(LLVM, "llvm-objdump"), "-d", "--mcpu=gfx950", str(co)], check=True,
-                         stdout=subprocess.PIPE, text=True).stdout
+    data = fatbin.read_bytes()
+    starts = []
+    i = data.find(BUNDLE_MAGIC)
+    while i >= 0:
+        starts.append(i)
+        i = data.find(BUNDLE_MAGIC, i + 1)
+    texts = []
+    for k, (lo, hi) in enumerate(zip(starts, starts[1:] + [len(data)])):
+        part, co = tmp_path / f"bundle{k}.bin", tmp_path / f"bundle{k}.co"
+        part.write_bytes(data[lo:hi])
+        subprocess.run([os.path.join(LLVM, "clang-offload-bundler"), "--unbundle", "--type=o", f"--input={part}",
+                        "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={co}"], check=True)
+        texts.append(subprocess.run([os.path.join(LLVM, "llvm-objdump"), "-d", "--mcpu=gfx950", str(co)],
+                                    check=True, stdout=subprocess.PIPE, text=True).stdout)
+    return texts
+
+
+def _instructions(dis):
     lines = []
     for raw in dis.splitlines():
         ins = raw.split("//")[0].strip()
         if ins and not ins.startswith(";") and not ins.endswith(":"):
             lines.append(ins)
-    n_dma = sum(1 for x in lines if x.startswith("global_load_lds"))
-    assert n_dma > 0
-    found = scan_lds_dma_hazards(lines)
-    assert not found, f"{len(found)} of {n_dma} LDS-DMA instructions read a VALU-written SGPR: {found[:3]}"
+    return lines
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="library not built")
+@pytest.mark.skipif(not all(os.path.exists(os.path.join(LLVM, t)) for t in TOOLS), reason="ROCm LLVM tools absent")
+def test_no_valu_sgpr_hazard_before_lds_dma(tmp_path):
+    texts = gfx950_disassembly(LIB, tmp_path)
+    assert len(texts) >= 2
+    # the quantize and the GEMM sources both copy through LDS-DMA
+    with_dma = [t for t in texts if "global_load_lds" in t]
+    assert any("fq_few2_kernel" in t for t in with_dma) and any("gemm_i4_pp2" in t for t in with_dma)
+    for dis in with_dma:
+        lines = _instructions(dis)
+        n_dma = sum(1 for x in lines if x.startswith("global_load_lds"))
+        found = scan_lds_dma_hazards(lines)
+        assert not found, f"{len(found)} of {n_dma} LDS-DMA instructions read a VALU-written SGPR: {found[:3]}"
