@@ -3,6 +3,10 @@
 // Replaces dequantize_int4 (flatquant/ops.py:156-178), which the reference runs
 // as eight strided torch passes for the packed layout. HBM-bound: 4 bytes of
 // packed codes (or 8 int8 codes) in, 32 bytes of float32 out per 8 features.
+// The vector kernels write with non-temporal stores (whole 16-byte pieces,
+// each store instruction 1 KiB of a row): the float32 output streams to memory
+// instead of waiting in L2 for the write-back at the kernel's end (config 2's
+// codes: 11.6 -> 7.6 us, same process, outputs equal).
 #include "common.h"
 
 namespace qo {
@@ -23,8 +27,8 @@ dequant_i8_kernel(const void* __restrict__ codes, const void* __restrict__ scale
       v[4 + j] = (float)(int8_t)((uint32_t)c[1] >> (8 * j)) * s;
     }
     v4f* o = reinterpret_cast<v4f*>(out + i * 8);
-    o[0] = v4f{v[0], v[1], v[2], v[3]};
-    o[1] = v4f{v[4], v[5], v[6], v[7]};
+    __builtin_nontemporal_store(v4f{v[0], v[1], v[2], v[3]}, o);
+    __builtin_nontemporal_store(v4f{v[4], v[5], v[6], v[7]}, o + 1);
   }
 }
 
@@ -51,7 +55,7 @@ dequant_rows_kernel(const int32_t* __restrict__ codes, const void* __restrict__ 
       v4f v;
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[j] = (float)((int)((bits >> (4 * j)) & 0xF) - 8) * s;
-      *reinterpret_cast<v4f*>(orow + w * 8 + 4 * sub) = v;
+      __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(orow + w * 8 + 4 * sub));
     }
   }
 }

@@ -1,5 +1,9 @@
 // Pack / unpack of int4 codes and the word transpose between the two layouts
-// of a packed weight. All three are HBM-bound byte work (no MFMA).
+// of a packed weight. All three are HBM-bound byte work (no MFMA). The vector
+// pack and unpack kernels write with non-temporal stores (the output streams
+// to memory instead of waiting in L2 for the write-back at the kernel's end;
+// config 4's weight, same process: pack 19.7 -> 18.8 us, unpack 18.8 -> 14.9);
+// the transpose gained nothing from them and keeps plain stores.
 //
 // * pack:   int8 codes [rows, F] -> int32 words [rows, F/8],
 //           word p = sum_i ((q[8p + i] + 8) mod 256) << 4i (mod 2^32)
@@ -39,7 +43,7 @@ pack_kernel_v16(const int8_t* __restrict__ codes, int64_t codes_ld, int64_t rows
     const int64_t r = i / pairs_per_row, p = i - r * pairs_per_row;
     const v4i c = *reinterpret_cast<const v4i*>(codes + r * codes_ld + 16 * p);
     const v2i w = {(int)pack_word((uint32_t)c[0], (uint32_t)c[1]), (int)pack_word((uint32_t)c[2], (uint32_t)c[3])};
-    *reinterpret_cast<v2i*>(out + r * out_ld + 2 * p) = w;
+    __builtin_nontemporal_store(w, reinterpret_cast<v2i*>(out + r * out_ld + 2 * p));
   }
 }
 
@@ -79,7 +83,7 @@ unpack_kernel_v16(const int32_t* __restrict__ words, int64_t words_ld, int64_t r
     const v2i w = *reinterpret_cast<const v2i*>(words + r * words_ld + 2 * p);
     const uint32_t w0 = (uint32_t)w[0], w1 = (uint32_t)w[1];
     const v4i c = {(int)unpack4(w0), (int)unpack4(w0 >> 16), (int)unpack4(w1), (int)unpack4(w1 >> 16)};
-    *reinterpret_cast<v4i*>(out + r * out_ld + 16 * p) = c;
+    __builtin_nontemporal_store(c, reinterpret_cast<v4i*>(out + r * out_ld + 16 * p));
   }
 }
 
