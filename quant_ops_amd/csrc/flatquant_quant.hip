@@ -1754,29 +1754,50 @@ __device__ inline void fq_wave_load_x(const typename DT::T* __restrict__ xt,
       xf[rb][ks] = *reinterpret_cast<const typename MfmaOps<DT>::V*>(xt + (16 * rb + li) * N + 32 * ks + 8 * lg);
 }
 
-// Store N adjacent 32-bit words (N = 1, 2 or 4) with one instruction.
-template <int NW_>
+// Store N adjacent 32-bit words (N = 1, 2 or 4) with one instruction,
+// non-temporal if NT.
+template <int NW_, bool NT>
 __device__ inline void store_words(int32_t* dst, const uint32_t (&w)[NW_]) {
   if constexpr (NW_ == 1) {
-    *dst = (int32_t)w[0];
+    if constexpr (NT) __builtin_nontemporal_store((int32_t)w[0], dst);
+    else *dst = (int32_t)w[0];
   } else if constexpr (NW_ == 2) {
-    *reinterpret_cast<v2i*>(dst) = v2i{(int)w[0], (int)w[1]};
+    const v2i v = {(int)w[0], (int)w[1]};
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<v2i*>(dst));
+    else *reinterpret_cast<v2i*>(dst) = v;
   } else {
     static_assert(NW_ == 4, "1, 2 or 4 words");
-    *reinterpret_cast<v4i*>(dst) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    const v4i v = {(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(dst));
+    else *reinterpret_cast<v4i*>(dst) = v;
   }
 }
 
 // Packed codes of a wave kernel token: lane (li, lg) writes row 16mb + li,
 // words NQ lg .. NQ lg + NQ - 1 (orow already offset by NQ lg).
-template <class DT, int MB, int NQ, bool LOW>
+template <class DT, int MB, int NQ, bool LOW, bool NT>
 __device__ inline void fq_wave_store_codes(int32_t* orow, const uint32_t (&yp)[MB][NQ][4], float rcp, int li) {
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     uint32_t words[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) words[q] = FqEpi<DT>::template word4<LOW>(yp[mb][q], rcp);
-    store_words<NQ>(orow + (16 * mb + li) * (4 * NQ), words);
+    store_words<NQ, NT>(orow + (16 * mb + li) * (4 * NQ), words);
+  }
+}
+
+// fq_wave_store_codes, non-temporal when nt (uniform). The empty asm
+// statements around the non-temporal branch keep the compiler from hoisting or
+// sinking its stores into the plain branch's (merged stores lose the flag).
+template <class DT, int MB, int NQ, bool LOW>
+__device__ inline void fq_wave_store_codes(int32_t* orow, const uint32_t (&yp)[MB][NQ][4], float rcp, int li,
+                                           bool nt) {
+  if (nt) {
+    asm volatile("" ::: "memory");
+    fq_wave_store_codes<DT, MB, NQ, LOW, true>(orow, yp, rcp, li);
+    asm volatile("" ::: "memory");
+  } else {
+    fq_wave_store_codes<DT, MB, NQ, LOW, false>(orow, yp, rcp, li);
   }
 }
 
@@ -1977,12 +1998,19 @@ fq_wave_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
     if (PACK && s > 0.f) {
       const float rcp = 1.0f / s;
       int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (F / 8) + NQ * lg;
+      // This wave's last token: its codes are written in the kernel's last
+      // microseconds, where plain stores would leave them dirty in L2 for the
+      // write-back at the kernel's end; non-temporal stores send them on
+      // (2048 tokens of 64 x 64 fp16, one per wave: 8.82 -> 7.66 us, same
+      // process). Earlier tokens keep plain stores, which L2 combines into
+      // whole lines (non-temporal for every token: 8192 tokens 22.7 -> 23.9 us).
+      const bool nt = tn >= tokens;
       // Quotients are >= -rnd(amax * rcp); below -8.5 they would need the
       // lower clamp (rne(-8.5) = -8). Uniform per token.
       if (DT::round(amax * rcp) > 8.5f)
-        fq_wave_store_codes<DT, MB, NQ, true>(orow, yp, rcp, li);
+        fq_wave_store_codes<DT, MB, NQ, true>(orow, yp, rcp, li, nt);
       else
-        fq_wave_store_codes<DT, MB, NQ, false>(orow, yp, rcp, li);
+        fq_wave_store_codes<DT, MB, NQ, false>(orow, yp, rcp, li, nt);
     } else {
       // int8 codes, and tokens whose scale rounded to 0 (the fallback's 0/0 codes)
       const float rcp = 1.0f / s;
