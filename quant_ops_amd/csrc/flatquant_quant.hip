@@ -1495,7 +1495,7 @@ struct FewLdsCompact {
   static_assert(STAGE_OFF % 16 == 0 && BYTES <= 80 * 1024, "two workgroups per CU");
 };
 
-template <class DT, int MB, bool PACK, bool NOCLAMP>
+template <class DT, int MB, bool PACK, bool NOCLAMP, bool STAGE>
 __device__ __attribute__((always_inline)) inline void few_quantize_compact(
     unsigned char* lds, const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
     const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
@@ -1588,16 +1588,50 @@ __device__ __attribute__((always_inline)) inline void few_quantize_compact(
   // memory operations retire in order, and after a token's copies every wave
   // issues at least MB code stores of the token before: waiting until at
   // most MB remain waits for the copies, not for those stores.
+  //
+  // STAGE (bf16 packed codes, 16-byte aligned output): a token's codes go to
+  // the staging area (free after the set-up) instead of memory, and the
+  // workgroup copies them out as whole 16-byte pieces of the token's
+  // contiguous codes during the next token, after its X request (so the wait
+  // at the top of a token still waits only for the copies: at least one store
+  // of every wave follows them). Without staging, each 64-byte row of codes
+  // is written in 16-byte parts by four waves. The last token's codes go out
+  // after the loop, non-temporal when the workgroup had more than one token
+  // (they would otherwise sit dirty in L2 for the write-back at the kernel's
+  // end; with one token per workgroup, the decode sizes, the next GEMM reads
+  // them at once and they stay plain). Measured (same process, outputs
+  // equal, two boxes): 8192 x 112 x 128 74.3 -> 73.0 / 78.6 -> 76.5 us,
+  // 4096 x 112 x 128 at clip 0.9 41.2 -> 39.8 / 42.3 -> 42.3, 8192 x 64 x 128
+  // 41.8 -> 39.9 / 44.2 -> 41.8; the linear step at 16 and 4096 tokens within
+  // the boxes' spread (15.8 -> 15.9, 195.0 -> 194.9 / 199.0 -> 200.1 us).
+  static_assert(!STAGE || (kEarly && PACK), "staging: bf16 packed codes");
+  int32_t* const cst = reinterpret_cast<int32_t*>(stage);
+  constexpr int PIECES = S::F / 32;   // 16-byte pieces of a token's packed codes
+  static_assert(S::F / 8 * 4 <= LD::STAGE_E * 2, "a token's codes fit the staging area");
+  auto store_staged = [&](int64_t tt, auto nt) {
+    const v4i* src = reinterpret_cast<const v4i*>(cst);
+    v4i* dst = reinterpret_cast<v4i*>(reinterpret_cast<int32_t*>(out_codes) + tt * (S::F / 8));
+#pragma unroll
+    for (int i = 0; i < (PIECES + 255) / 256; ++i) {
+      const int pc = tid + 256 * i;
+      if (pc < PIECES) {
+        if constexpr (decltype(nt)::value) __builtin_nontemporal_store(src[pc], dst + pc);
+        else dst[pc] = src[pc];
+      }
+    }
+  };
+  static_assert(!STAGE || PIECES > 192, "every wave stores at least one piece per staged token");
   for (; t < tokens; t += groups) {
-    if (t == group) wait_vmcnt<0>();
-    else wait_vmcnt<MB>();
+    if (t == group || (STAGE && t == group + groups)) wait_vmcnt<0>();
+    else wait_vmcnt<(STAGE ? 1 : MB)>();
     raw_barrier();
     uint32_t yp[MB][4];
     float amax, amax_d;
     if constexpr (kEarly) {
       few_products<DT, MB, kG>(xb, lfrag, rf, lane, yp, amax, [&]() {
-        lds_barrier();   // every wave's reads of X are done
+        lds_barrier();   // every wave's reads of X (and of the staged codes' previous readers) are done
         if (t + groups < tokens) issue(t + groups);
+        if (STAGE && t != group) store_staged(t - groups, std::false_type{});
       });
     } else {
       few_products<DT, MB, kG>(xb, lfrag, rf, lane, yp, amax);
@@ -1606,12 +1640,18 @@ __device__ __attribute__((always_inline)) inline void few_quantize_compact(
     if (!kEarly && t + groups < tokens) issue(t + groups);
     if (q == 0 && lane == 0) out_scales[t] = sc;
     if constexpr (PACK) {
-      int32_t* orow = reinterpret_cast<int32_t*>(out_codes) + t * (S::F / 8) + 4 * q + lg;
+      int32_t* orow = (STAGE ? cst : reinterpret_cast<int32_t*>(out_codes) + t * (S::F / 8)) + 4 * q + lg;
       few_codes_packed<DT, MB, NOCLAMP>(yp, 1.0f / sc, orow, li);
       if (!(sc > 0.f)) few_codes_zero_scale<DT, MB>(yp, sc, orow, li);
     } else {
       few_codes_int8<DT, MB>(yp, sc, reinterpret_cast<int8_t*>(out_codes) + t * S::F + 32 * q + 8 * lg, li);
     }
+  }
+  if constexpr (STAGE) {
+    lds_barrier();   // the last token's codes are staged
+    const int64_t last = group + (tokens - 1 - group) / groups * groups;
+    if (last != group) store_staged(last, std::true_type{});
+    else store_staged(last, std::false_type{});
   }
   wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
 }
@@ -1664,7 +1704,7 @@ __device__ inline void read_ahead_rows(const v4i* __restrict__ p, int64_t rows, 
 // Workgroups 0 .. qgroups - 1 quantize; the rest, if any, read ahead.
 // NOCLAMP (bf16, packed codes): the host has found from the clip ratio that no
 // quotient can round to 7.5 or above (kNoClampClip).
-template <class DT, int MB, bool PACK, bool NOCLAMP = false>
+template <class DT, int MB, bool PACK, bool NOCLAMP = false, bool STAGE = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fq_few2_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_ld,
                const typename DT::T* __restrict__ left, const typename DT::T* __restrict__ right, float clip,
@@ -1675,8 +1715,8 @@ fq_few2_kernel(const typename DT::T* __restrict__ x, int64_t tokens, int64_t x_l
     read_ahead_rows(ahead, ahead_rows, ahead_rs16, ahead_len16, qgroups);
     return;
   }
-  few_quantize_compact<DT, MB, PACK, NOCLAMP>(lds, x, tokens, x_ld, left, right, clip, out_codes, out_scales,
-                                              blockIdx.x, qgroups);
+  few_quantize_compact<DT, MB, PACK, NOCLAMP, STAGE>(lds, x, tokens, x_ld, left, right, clip, out_codes,
+                                                     out_scales, blockIdx.x, qgroups);
 }
 
 // ---------------------------------------------------------------------------
@@ -2445,10 +2485,16 @@ static int launch_few(const void* x, int64_t tokens, int64_t x_ld, const void* l
              ra.row_bytes / 16, ahead ? (int)(ra.row_len / 16) : 0);
     };
     if constexpr (std::is_same<DT, BF16T>::value && PACK) {
+      // staged code stores need 16-byte pieces of the codes
+      const bool stage = (uintptr_t)out_codes % 16 == 0;
       if (clip >= kNoClampClip) {
-        go(fq_few2_kernel<DT, MB, PACK, true>);
-        return QO_OK;
+        if (stage) go(fq_few2_kernel<DT, MB, PACK, true, true>);
+        else go(fq_few2_kernel<DT, MB, PACK, true>);
+      } else {
+        if (stage) go(fq_few2_kernel<DT, MB, PACK, false, true>);
+        else go(fq_few2_kernel<DT, MB, PACK>);
       }
+      return QO_OK;
     }
     go(fq_few2_kernel<DT, MB, PACK>);
     return QO_OK;
