@@ -480,7 +480,7 @@ def cpu_dequant(torch, budget_s):
 KERNEL_OF = {
     "gemm_cfg4": "gemm_i4_pp2<256, 224, false, qo::OutF16>",
     "quantize_cfg2": "fq_wave_kernel<qo::F16T, 4, 2, true>",
-    "quantize_cfg3": "fq_few2_kernel<qo::BF16T, 7, true, true>",
+    "quantize_cfg3": "fq_few2_kernel<qo::BF16T, 7, true, true, true>",
     "gemm_cfg5_T16": "gemm_i4_skinny_nk",
     "gemm_cfg5_T4096": "gemm_i4_pp2<256, 256, true, qo::OutBF16>",
 }
