@@ -1650,8 +1650,15 @@ __device__ __attribute__((always_inline)) inline void few_quantize_compact(
   if constexpr (STAGE) {
     lds_barrier();   // the last token's codes are staged
     const int64_t last = group + (tokens - 1 - group) / groups * groups;
-    if (last != group) store_staged(last, std::true_type{});
-    else store_staged(last, std::false_type{});
+    if (last != group) {
+      // fenced so that the compiler cannot merge these stores with the plain
+      // branch's (a merged store loses the non-temporal flag)
+      asm volatile("" ::: "memory");
+      store_staged(last, std::true_type{});
+      asm volatile("" ::: "memory");
+    } else {
+      store_staged(last, std::false_type{});
+    }
   }
   wait_vmcnt<0>();  // no LDS-DMA may still be writing when the workgroup retires
 }
