@@ -68,7 +68,8 @@ enum qo_route {
   QO_ROUTE_GEMM_NO_DMA = 1u << 5,    /* GEMM: no LDS-DMA tiled kernel */
   QO_ROUTE_GEMM_NO_SKINNY = 1u << 6, /* GEMM: no small-M kernels */
   QO_ROUTE_LINEAR_NO_READ_AHEAD = 1u << 7, /* linear: no weight read-ahead in the quantize launch */
-  QO_ROUTE_ALL = (1u << 8) - 1u
+  QO_ROUTE_GEMM_NO_F6 = 1u << 8,     /* GEMM: no FP6 matrix-core route (qo_int4_gemm_ws) */
+  QO_ROUTE_ALL = (1u << 9) - 1u
 };
 unsigned qo_set_kernel_routing(unsigned mask);
 
@@ -146,6 +147,73 @@ int qo_int4_gemm_bias(const int32_t* a, int64_t lda,
                       const void* bias,
                       void* out, int out_dtype, int64_t ldc,
                       int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * qo_int4_gemm (bias may be NULL, else as qo_int4_gemm_bias) with a caller
+ * workspace, which lets large products take the FP6 matrix-core route: the
+ * int4 codes of A and B are rewritten into the workspace as FP6 e2m3 values
+ * q / 8 (exact), then multiplied on v_mfma_scale_f32_16x16x128_f8f6f4 with
+ * block scales 2^3, whose float32 sums equal the exact int32 sums; the
+ * outputs are bit for bit those of qo_int4_gemm. The same entry point as
+ * cuda_int4_matmul (cuda_int4_matmul_kernel.cu:130-189), which needs no
+ * workspace; the torch operator int4_matmul allocates it.
+ *
+ *   workspace        device memory, 256-byte aligned, workspace_bytes long;
+ *                    only read and written by this call's kernels on stream
+ *                    (calls sharing a workspace must be ordered)
+ *   workspace_bytes  at least qo_int4_gemm_workspace_size(M, N, K, out_dtype)
+ *                    for the FP6 route; a smaller (or NULL) workspace takes
+ *                    qo_int4_gemm's kernels
+ *
+ * Errors: those of qo_int4_gemm.
+ */
+int qo_int4_gemm_ws(const int32_t* a, int64_t lda,
+                    const int32_t* b, int64_t b_stride_p, int64_t b_stride_n,
+                    const void* scale_a, int scale_a_dtype,
+                    const void* scale_b, int scale_b_dtype,
+                    const void* bias,
+                    void* out, int out_dtype, int64_t ldc,
+                    int64_t M, int64_t N, int64_t K,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes qo_int4_gemm_ws uses for an M x N x K product with outputs
+ * of out_dtype: 0 when the shape does not take the FP6 route (M <= 256, float32
+ * outputs, K > 65536, or QO_ROUTE_GEMM_NO_F6 or QO_ROUTE_GEMM_GENERIC set), else
+ * qo_int4_gemm_f6_workspace_bytes(M, N, K): 0.75 (M + N) K bytes plus padding
+ * (M and N up to multiples of 32, K up to a multiple of 128).
+ */
+int64_t qo_int4_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int out_dtype);
+
+/*
+ * The two launches of qo_int4_gemm_ws's FP6 route, for callers that keep one
+ * operand converted (a weight converted once and multiplied many times) or
+ * time the kernels apart. No counterpart in the reference.
+ *
+ * qo_int4_gemm_f6_prepare converts A (a, lda as qo_int4_gemm) and / or B (b
+ * and its strides as qo_int4_gemm, one of them 1) into the workspace; a NULL
+ * a or b leaves that operand's part of the workspace as it is.
+ * qo_int4_gemm_f6_run multiplies the two operands held in the workspace:
+ * out = rnd((acc * sa[m]) * sb[n]) (+ bias as qo_int4_gemm_bias, bias may be
+ * NULL), out_dtype F16 or BF16; bit for bit qo_int4_gemm's result for the
+ * same codes. Both take any M, N >= 1 and K (multiple of 8) <= 65536, and
+ * a workspace of qo_int4_gemm_f6_workspace_bytes(M, N, K) bytes, 256-byte
+ * aligned; the workspace layout is internal and depends on (M, N, K) only.
+ *
+ * Errors: QO_ERR_SHAPE for sizes outside those bounds, a small or misaligned
+ * workspace, lda or ldc too small, or B with no unit stride;
+ * QO_ERR_NULL_POINTER; QO_ERR_DTYPE (run: other out_dtype codes).
+ */
+int64_t qo_int4_gemm_f6_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int qo_int4_gemm_f6_prepare(const int32_t* a, int64_t lda,
+                            const int32_t* b, int64_t b_stride_p, int64_t b_stride_n,
+                            int64_t M, int64_t N, int64_t K,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+int qo_int4_gemm_f6_run(const void* scale_a, int scale_a_dtype,
+                        const void* scale_b, int scale_b_dtype,
+                        const void* bias, void* out, int out_dtype, int64_t ldc,
+                        int64_t M, int64_t N, int64_t K,
+                        const void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * W4A4 FlatQuant linear layer: per-token dynamic quantization of x with the

@@ -26,7 +26,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OBJ = os.path.join(HERE, "_obj")
 
-HIP_SOURCES = ["capi.hip", "flatquant_quant.hip", "int4_gemm.hip", "dequant.hip", "layout.hip", "w4a4_linear.hip"]
+HIP_SOURCES = ["capi.hip", "flatquant_quant.hip", "int4_gemm.hip", "int4_gemm_f6.hip", "dequant.hip", "layout.hip", "w4a4_linear.hip"]
 LIB_NAME = "libquant_ops_hip.so"
 TORCH_LIB_NAME = "_quant_ops_torch.so"
 # microbenchmarks of the hardware ceilings (bench.py --ceilings), a library of its own

@@ -20,13 +20,14 @@ STATUS = {0: "QO_OK", 1: "QO_ERR_NULL_POINTER", 2: "QO_ERR_SHAPE", 3: "QO_ERR_DT
 
 # Every symbol the header declares; the CPU tests check they are all exported.
 EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_set_kernel_routing", "qo_flatquant_quantize",
-            "qo_int4_gemm", "qo_int4_gemm_bias", "qo_w4a4_linear", "qo_w4a4_linear_noalloc", "qo_dequantize_int4",
+            "qo_int4_gemm", "qo_int4_gemm_bias", "qo_int4_gemm_ws", "qo_int4_gemm_workspace_size", "qo_int4_gemm_f6_workspace_bytes",
+            "qo_int4_gemm_f6_prepare", "qo_int4_gemm_f6_run", "qo_w4a4_linear", "qo_w4a4_linear_noalloc", "qo_dequantize_int4",
             "qo_pack_int4_to_int32", "qo_unpack_int32_to_int4", "qo_transpose_int32")
 
 # QO_ROUTE_* bits of qo_set_kernel_routing (include/quant_ops_hip.h)
 ROUTE = {"FQ_GENERIC": 1 << 0, "FQ_NO_WAVE": 1 << 1, "FQ_NO_DUO": 1 << 2, "FQ_NO_FEW": 1 << 3,
          "GEMM_GENERIC": 1 << 4, "GEMM_NO_DMA": 1 << 5, "GEMM_NO_SKINNY": 1 << 6,
-         "LINEAR_NO_READ_AHEAD": 1 << 7}
+         "LINEAR_NO_READ_AHEAD": 1 << 7, "GEMM_NO_F6": 1 << 8}
 
 _TORCH_CODE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
@@ -66,6 +67,18 @@ def lib():
     L.qo_int4_gemm_bias.restype = c_int
     L.qo_int4_gemm_bias.argtypes = [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int,
                                     c_i64, c_i64, c_i64, c_i64, c_vp]
+    L.qo_int4_gemm_ws.restype = c_int
+    L.qo_int4_gemm_ws.argtypes = [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int,
+                                  c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp]
+    L.qo_int4_gemm_workspace_size.restype = c_i64
+    L.qo_int4_gemm_workspace_size.argtypes = [c_i64, c_i64, c_i64, c_int]
+    L.qo_int4_gemm_f6_workspace_bytes.restype = c_i64
+    L.qo_int4_gemm_f6_workspace_bytes.argtypes = [c_i64, c_i64, c_i64]
+    L.qo_int4_gemm_f6_prepare.restype = c_int
+    L.qo_int4_gemm_f6_prepare.argtypes = [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp]
+    L.qo_int4_gemm_f6_run.restype = c_int
+    L.qo_int4_gemm_f6_run.argtypes = [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp,
+                                      c_i64, c_vp]
     L.qo_w4a4_linear.restype = c_int
     L.qo_w4a4_linear.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_vp, c_i64, c_i64,
                                  c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]
@@ -147,9 +160,17 @@ def flatquant_quantize(x, left, right, clip_ratio=1.0, pack_int32=False, out_cod
     return out_codes, out_scales
 
 
-def int4_gemm(a, b, scale_a, scale_b, out_dtype=torch.float16, out=None, stream=None, bias=None):
+def gemm_workspace_size(m, n, k, out_dtype=torch.float16):
+    """``qo_int4_gemm_workspace_size``: bytes of the FP6 route's workspace (0: not taken)."""
+    return int(lib().qo_int4_gemm_workspace_size(m, n, k, _TORCH_CODE[out_dtype]))
+
+
+def int4_gemm(a, b, scale_a, scale_b, out_dtype=torch.float16, out=None, stream=None, bias=None,
+              workspace=None):
     """Call ``qo_int4_gemm`` (``qo_int4_gemm_bias`` with ``bias``, converted to the
-    output dtype); ``b`` may be row-major [K/8, N] or the ``W.t()`` view."""
+    output dtype); ``b`` may be row-major [K/8, N] or the ``W.t()`` view. With
+    ``workspace`` (a uint8 device tensor, or True to allocate one of
+    gemm_workspace_size bytes) the call goes to ``qo_int4_gemm_ws``."""
     m, kp = a.shape
     if a.stride(1) != 1:
         a = a.contiguous()
@@ -165,11 +186,53 @@ def int4_gemm(a, b, scale_a, scale_b, out_dtype=torch.float16, out=None, stream=
             ctypes.c_void_p(scale_b.data_ptr()), _TORCH_CODE[scale_b.dtype])
     tail = (ctypes.c_void_p(out.data_ptr()), _TORCH_CODE[out.dtype], out.stride(0) if m else n,
             m, n, kp * 8, _stream(stream))
-    if bias is None:
+    if bias is not None:
+        bias = bias.to(out.dtype).contiguous()
+    if workspace is not None:
+        if workspace is True:
+            workspace = torch.empty(max(1, gemm_workspace_size(m, n, kp * 8, out.dtype)), dtype=torch.uint8,
+                                    device=a.device)
+        _check(lib().qo_int4_gemm_ws(*head, ctypes.c_void_p(bias.data_ptr() if bias is not None else None),
+                                     *tail[:-1], ctypes.c_void_p(workspace.data_ptr()), workspace.numel(),
+                                     tail[-1]))
+    elif bias is None:
         _check(lib().qo_int4_gemm(*head, *tail))
     else:
-        bias = bias.to(out.dtype).contiguous()
         _check(lib().qo_int4_gemm_bias(*head, ctypes.c_void_p(bias.data_ptr()), *tail))
+    return out
+
+
+def f6_workspace_bytes(m, n, k):
+    """``qo_int4_gemm_f6_workspace_bytes``."""
+    return int(lib().qo_int4_gemm_f6_workspace_bytes(m, n, k))
+
+
+def f6_prepare(workspace, m, n, k, a=None, b=None, stream=None):
+    """``qo_int4_gemm_f6_prepare``: convert A [M, K/8] and / or B ([K/8, N] or the
+    ``W.t()`` view) into ``workspace`` (uint8 device tensor)."""
+    if a is not None and a.stride(1) != 1:
+        a = a.contiguous()
+    if b is not None and b.stride(0) != 1 and b.stride(1) != 1:
+        b = b.contiguous()
+    _check(lib().qo_int4_gemm_f6_prepare(
+        ctypes.c_void_p(a.data_ptr() if a is not None else None), a.stride(0) if a is not None else 0,
+        ctypes.c_void_p(b.data_ptr() if b is not None else None), b.stride(0) if b is not None else 0,
+        b.stride(1) if b is not None else 0, m, n, k, ctypes.c_void_p(workspace.data_ptr()), workspace.numel(),
+        _stream(stream)))
+
+
+def f6_run(workspace, m, n, k, scale_a, scale_b, out_dtype=torch.float16, out=None, bias=None, stream=None):
+    """``qo_int4_gemm_f6_run`` on a prepared ``workspace``; returns out [M, N]."""
+    scale_a, scale_b = scale_a.contiguous(), scale_b.contiguous()
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=workspace.device)
+    if bias is not None:
+        bias = bias.to(out.dtype).contiguous()
+    _check(lib().qo_int4_gemm_f6_run(
+        ctypes.c_void_p(scale_a.data_ptr()), _TORCH_CODE[scale_a.dtype], ctypes.c_void_p(scale_b.data_ptr()),
+        _TORCH_CODE[scale_b.dtype], ctypes.c_void_p(bias.data_ptr() if bias is not None else None),
+        ctypes.c_void_p(out.data_ptr()), _TORCH_CODE[out.dtype], out.stride(0), m, n, k,
+        ctypes.c_void_p(workspace.data_ptr()), workspace.numel(), _stream(stream)))
     return out
 
 

@@ -112,4 +112,76 @@ __device__ inline void with_scale_dtype(int code, F&& f) {
   else f(std::integral_constant<int, QO_DTYPE_BF16>{});
 }
 
+// vmcnt waits of the pipelined kernels' LDS-DMA rings.
+template <int N>
+__device__ inline void gemm_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Wait until at most n groups of G copies are in flight, n a workgroup-uniform
+// runtime count clamped to 0 .. MAXN (the counter takes only constants).
+template <int G, int MAXN>
+__device__ inline void gemm_wait_groups(int n) {
+  if constexpr (MAXN <= 0) {
+    gemm_wait_vmcnt<0>();
+  } else {
+    if (n >= MAXN) gemm_wait_vmcnt<G * MAXN>();
+    else gemm_wait_groups<G, MAXN - 1>(n);
+  }
+}
+
+// Output value of a 16-bit type as its bit pattern.
+template <class OT>
+__device__ inline uint32_t out_bits(typename OT::T v) {
+  return (uint32_t)(uint16_t)__builtin_bit_cast(uint16_t, v);
+}
+
+// Second half of the staged epilogue of the tiled kernels: the workgroup copies the BM x BN tile of 16-bit values from LDS
+// to C in 16-byte pieces, consecutive threads taking consecutive pieces of a
+// row (rows and columns past the matrix edge are skipped; C rows that are not
+// 16-byte aligned take element stores).
+template <int BM, int BN, int THREADS, class OT>
+__device__ __attribute__((always_inline)) inline void copy_out_c(const unsigned char* c_tile, int pitch, typename OT::T* out, int64_t ldc, int M,
+                                  int N, int m0, int n0, int tid) {
+  using T = typename OT::T;
+  constexpr int PPR = BN * 2 / 16;   // 16-byte pieces per row
+  static_assert(BN % 8 == 0 && (BM * PPR) % THREADS == 0, "pieces");
+  const bool vec = ((uintptr_t)out % 16 == 0) && (ldc % 8 == 0);
+#pragma unroll
+  for (int it = 0; it < BM * PPR / THREADS; ++it) {
+    const int p = tid + THREADS * it;
+    const int row = p / PPR, q = p % PPR;
+    const int m = m0 + row, n = n0 + 8 * q;
+    if (m >= M || n >= N) continue;
+    const v4i d = *reinterpret_cast<const v4i*>(c_tile + row * pitch + 16 * q);
+    T* o = out + (int64_t)m * ldc + n;
+    if (vec && n + 7 < N) {
+      *reinterpret_cast<v4i*>(o) = d;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N) o[e] = __builtin_bit_cast(T, (uint16_t)((uint32_t)d[e / 2] >> (16 * (e % 2))));
+    }
+  }
+}
+
+// The FP6 route of the tiled GEMM (int4_gemm_f6.hip): workspace bytes for an
+// M x N x K product, and the two launches (operand conversion into the
+// workspace, then the FP6 GEMM) for 16-bit outputs, M >= 1, N >= 1,
+// K <= 65536 and any strides of A and B.
+int64_t f6_workspace_bytes(int64_t M, int64_t N, int64_t K);
+template <class OT>
+void f6_gemm_launch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, int64_t bsn, const void* sa,
+                    int sad, const void* sb, int sbd, typename OT::T* out, int64_t ldc, const typename OT::T* bias,
+                    int64_t M, int64_t N, int64_t K, void* workspace, hipStream_t stream);
+// The two halves of f6_gemm_launch: the conversion of A and / or B (either
+// pointer null: that operand is left as it is in the workspace), and the GEMM
+// on a workspace holding both.
+void f6_prepare(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, int64_t bsn, int64_t M, int64_t N,
+                int64_t K, void* workspace, hipStream_t stream);
+template <class OT>
+void f6_run(const void* sa, int sad, const void* sb, int sbd, typename OT::T* out, int64_t ldc,
+            const typename OT::T* bias, int64_t M, int64_t N, int64_t K, const void* workspace, hipStream_t stream);
+
 }  // namespace qo

@@ -303,24 +303,6 @@ struct DmaStage {
   static_assert(B_NK || BN <= 256, "a KN row of the tile must fit one 1 KiB DMA");
 };
 
-template <int N>
-__device__ inline void gemm_wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt out of range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// Wait until at most n groups of G copies are in flight, n a workgroup-uniform
-// runtime count clamped to 0 .. MAXN (the counter takes only constants).
-template <int G, int MAXN>
-__device__ inline void gemm_wait_groups(int n) {
-  if constexpr (MAXN <= 0) {
-    gemm_wait_vmcnt<0>();
-  } else {
-    if (n >= MAXN) gemm_wait_vmcnt<G * MAXN>();
-    else gemm_wait_groups<G, MAXN - 1>(n);
-  }
-}
-
 // Which output columns a wave's FN accumulator blocks hold. A block's 16
 // "rows" in the transposed product are 16 B columns, one per lane li of its
 // operand. Plain (IL false): block j holds columns 16j .. 16j + 15 of the
@@ -405,12 +387,6 @@ __device__ inline void store_c_lds(const v4i (&acc)[FM][WN / 16], const float* s
   }
 }
 
-// Output value of a 16-bit type as its bit pattern.
-template <class OT>
-__device__ inline uint32_t out_bits(typename OT::T v) {
-  return (uint32_t)(uint16_t)__builtin_bit_cast(uint16_t, v);
-}
-
 // First half of the staged epilogue: the wave's values (scaled, rounded, bias
 // added as in store_c_lds) written as 8-byte runs into an LDS tile; c_tile
 // points at the wave's first row and column, pitch in bytes.
@@ -437,35 +413,6 @@ __device__ __attribute__((always_inline)) inline void stage_c(const v4i (&acc)[F
       }
       *reinterpret_cast<v2i*>(c_tile + (16 * i + li) * pitch + 2 * c) =
           v2i{(int)(out_bits<OT>(v[0]) | out_bits<OT>(v[1]) << 16), (int)(out_bits<OT>(v[2]) | out_bits<OT>(v[3]) << 16)};
-    }
-  }
-}
-
-// Second half: the workgroup copies the BM x BN tile of 16-bit values from LDS
-// to C in 16-byte pieces, consecutive threads taking consecutive pieces of a
-// row (rows and columns past the matrix edge are skipped; C rows that are not
-// 16-byte aligned take element stores).
-template <int BM, int BN, int THREADS, class OT>
-__device__ __attribute__((always_inline)) inline void copy_out_c(const unsigned char* c_tile, int pitch, typename OT::T* out, int64_t ldc, int M,
-                                  int N, int m0, int n0, int tid) {
-  using T = typename OT::T;
-  constexpr int PPR = BN * 2 / 16;   // 16-byte pieces per row
-  static_assert(BN % 8 == 0 && (BM * PPR) % THREADS == 0, "pieces");
-  const bool vec = ((uintptr_t)out % 16 == 0) && (ldc % 8 == 0);
-#pragma unroll
-  for (int it = 0; it < BM * PPR / THREADS; ++it) {
-    const int p = tid + THREADS * it;
-    const int row = p / PPR, q = p % PPR;
-    const int m = m0 + row, n = n0 + 8 * q;
-    if (m >= M || n >= N) continue;
-    const v4i d = *reinterpret_cast<const v4i*>(c_tile + row * pitch + 16 * q);
-    T* o = out + (int64_t)m * ldc + n;
-    if (vec && n + 7 < N) {
-      *reinterpret_cast<v4i*>(o) = d;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (n + e < N) o[e] = __builtin_bit_cast(T, (uint16_t)((uint32_t)d[e / 2] >> (16 * (e % 2))));
     }
   }
 }
@@ -1413,11 +1360,28 @@ static void launch_skinny(const int32_t* a, int64_t lda, const int32_t* b, int64
   else by_layout(std::integral_constant<int, 8>{});
 }
 
+// Shapes that take the FP6 route when the caller gives a workspace: the
+// tiled shapes (more than 256 rows; fewer take the small-M kernels), 16-bit
+// outputs, B with one unit stride, K within the exact float32 range.
+static bool f6_route(int64_t M, int64_t N, int64_t K, int out_dtype, int64_t bsp, int64_t bsn) {
+  return (out_dtype == QO_DTYPE_F16 || out_dtype == QO_DTYPE_BF16) && M > 256 && N >= 1 && K >= 8 && K <= 65536 &&
+         M <= INT32_MAX / 2 && N <= INT32_MAX / 2 && (bsp == 1 || bsn == 1) && !route_off(QO_ROUTE_GEMM_NO_F6);
+}
+
 template <class OT>
 static void dispatch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, int64_t bsn, const void* sa,
                      int sad, const void* sb, int sbd, void* out, int64_t ldc, const void* bias, int64_t M, int64_t N, int64_t K,
-                     hipStream_t stream, bool allow_fast) {
+                     hipStream_t stream, bool allow_fast, void* workspace, int64_t ws_bytes) {
   using T = typename OT::T;
+  if constexpr (sizeof(T) == 2) {
+    if (allow_fast && workspace && (uintptr_t)workspace % 256 == 0 &&
+        f6_route(M, N, K, std::is_same_v<OT, OutF16> ? QO_DTYPE_F16 : QO_DTYPE_BF16, bsp, bsn) &&
+        ws_bytes >= f6_workspace_bytes(M, N, K)) {
+      f6_gemm_launch<OT>(a, lda, b, bsp, bsn, sa, sad, sb, sbd, static_cast<T*>(out), ldc,
+                         static_cast<const T*>(bias), M, N, K, workspace, stream);
+      return;
+    }
+  }
   const bool b_nk = (bsp == 1);
   const bool b_kn = (bsn == 1) && !b_nk;
   const int64_t ldb = b_nk ? bsn : bsp;
@@ -1481,7 +1445,7 @@ static bool is_float_code(int d) { return d == QO_DTYPE_F32 || d == QO_DTYPE_F16
 static int gemm_entry(const char* who, const int32_t* a, int64_t lda, const int32_t* b, int64_t b_stride_p,
                       int64_t b_stride_n, const void* scale_a, int scale_a_dtype, const void* scale_b,
                       int scale_b_dtype, void* out, int out_dtype, int64_t ldc, const void* bias, int64_t M,
-                      int64_t N, int64_t K, void* stream) {
+                      int64_t N, int64_t K, void* stream, void* workspace = nullptr, int64_t ws_bytes = 0) {
   using namespace qo;
   if (M < 0 || N < 0 || K < 0 || (K % 8) != 0) {
     qo_set_error("%s: invalid sizes M=%lld N=%lld K=%lld (K must be a multiple of 8)", who, (long long)M,
@@ -1512,15 +1476,15 @@ static int gemm_entry(const char* who, const int32_t* a, int64_t lda, const int3
   switch (out_dtype) {
     case QO_DTYPE_F16:
       dispatch<OutF16>(a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b, scale_b_dtype, out, ldc,
-                       bias, M, N, K, s, fast);
+                       bias, M, N, K, s, fast, workspace, ws_bytes);
       break;
     case QO_DTYPE_BF16:
       dispatch<OutBF16>(a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b, scale_b_dtype, out,
-                        ldc, bias, M, N, K, s, fast);
+                        ldc, bias, M, N, K, s, fast, workspace, ws_bytes);
       break;
     default:
       dispatch<OutF32>(a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b, scale_b_dtype, out, ldc,
-                       bias, M, N, K, s, fast);
+                       bias, M, N, K, s, fast, workspace, ws_bytes);
       break;
   }
   return launch_result(who);
@@ -1544,4 +1508,93 @@ extern "C" int qo_int4_gemm_bias(const int32_t* a, int64_t lda, const int32_t* b
   }
   return gemm_entry("qo_int4_gemm_bias", a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b,
                     scale_b_dtype, out, out_dtype, ldc, bias, M, N, K, stream);
+}
+
+extern "C" int qo_int4_gemm_ws(const int32_t* a, int64_t lda, const int32_t* b, int64_t b_stride_p,
+                               int64_t b_stride_n, const void* scale_a, int scale_a_dtype, const void* scale_b,
+                               int scale_b_dtype, const void* bias, void* out, int out_dtype, int64_t ldc, int64_t M,
+                               int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+  return gemm_entry("qo_int4_gemm_ws", a, lda, b, b_stride_p, b_stride_n, scale_a, scale_a_dtype, scale_b,
+                    scale_b_dtype, out, out_dtype, ldc, bias, M, N, K, stream, workspace, workspace_bytes);
+}
+
+extern "C" int64_t qo_int4_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int out_dtype) {
+  // sized for either B layout (the route also needs one unit stride of B)
+  if (!gemm_allow_fast() || K % 8 != 0 || !qo::f6_route(M, N, K, out_dtype, 1, 0)) return 0;
+  return qo::f6_workspace_bytes(M, N, K);
+}
+
+// Checks shared by the two halves of the FP6 route.
+static int f6_check(const char* who, int64_t M, int64_t N, int64_t K, const void* workspace, int64_t ws_bytes) {
+  if (M < 1 || N < 1 || K < 8 || K % 8 != 0 || K > 65536 || M > INT32_MAX / 2 || N > INT32_MAX / 2) {
+    qo_set_error("%s: sizes M=%lld N=%lld K=%lld outside the FP6 route (M, N >= 1, K a multiple of 8 in 8 .. 65536)",
+                 who, (long long)M, (long long)N, (long long)K);
+    return QO_ERR_SHAPE;
+  }
+  if (!workspace) {
+    qo_set_error("%s: NULL workspace", who);
+    return QO_ERR_NULL_POINTER;
+  }
+  if ((uintptr_t)workspace % 256 != 0 || ws_bytes < qo::f6_workspace_bytes(M, N, K)) {
+    qo_set_error("%s: workspace not 256-byte aligned or smaller than %lld bytes", who,
+                 (long long)qo::f6_workspace_bytes(M, N, K));
+    return QO_ERR_SHAPE;
+  }
+  return QO_OK;
+}
+
+extern "C" int qo_int4_gemm_f6_prepare(const int32_t* a, int64_t lda, const int32_t* b, int64_t b_stride_p,
+                                       int64_t b_stride_n, int64_t M, int64_t N, int64_t K, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  const char* who = "qo_int4_gemm_f6_prepare";
+  const int st = f6_check(who, M, N, K, workspace, workspace_bytes);
+  if (st != QO_OK) return st;
+  if (a && lda < K / 8) {
+    qo_set_error("%s: lda=%lld below K/8", who, (long long)lda);
+    return QO_ERR_SHAPE;
+  }
+  if (b && b_stride_p != 1 && b_stride_n != 1) {
+    qo_set_error("%s: B needs a unit stride (row-major [K/8, N] or the W.t() view)", who);
+    return QO_ERR_SHAPE;
+  }
+  qo::launch_begin();
+  qo::f6_prepare(a, lda, b, b_stride_p, b_stride_n, M, N, K, workspace, reinterpret_cast<hipStream_t>(stream));
+  return qo::launch_result(who);
+}
+
+extern "C" int qo_int4_gemm_f6_run(const void* scale_a, int scale_a_dtype, const void* scale_b, int scale_b_dtype,
+                                   const void* bias, void* out, int out_dtype, int64_t ldc, int64_t M, int64_t N,
+                                   int64_t K, const void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace qo;
+  const char* who = "qo_int4_gemm_f6_run";
+  const int st = f6_check(who, M, N, K, workspace, workspace_bytes);
+  if (st != QO_OK) return st;
+  if (!is_float_code(scale_a_dtype) || !is_float_code(scale_b_dtype) ||
+      (out_dtype != QO_DTYPE_F16 && out_dtype != QO_DTYPE_BF16)) {
+    qo_set_error("%s: unsupported dtype codes (scale_a=%d, scale_b=%d, out=%d; out must be F16 or BF16)", who,
+                 scale_a_dtype, scale_b_dtype, out_dtype);
+    return QO_ERR_DTYPE;
+  }
+  if (ldc < N) {
+    qo_set_error("%s: ldc=%lld below N", who, (long long)ldc);
+    return QO_ERR_SHAPE;
+  }
+  if (!scale_a || !scale_b || !out) {
+    qo_set_error("%s: NULL pointer argument", who);
+    return QO_ERR_NULL_POINTER;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  launch_begin();
+  if (out_dtype == QO_DTYPE_F16)
+    f6_run<OutF16>(scale_a, scale_a_dtype, scale_b, scale_b_dtype, static_cast<_Float16*>(out), ldc,
+                   static_cast<const _Float16*>(bias), M, N, K, workspace, s);
+  else
+    f6_run<OutBF16>(scale_a, scale_a_dtype, scale_b, scale_b_dtype, static_cast<__bf16*>(out), ldc,
+                    static_cast<const __bf16*>(bias), M, N, K, workspace, s);
+  return launch_result(who);
+}
+
+extern "C" int64_t qo_int4_gemm_f6_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < 1 || K < 8 || K > 65536) return 0;
+  return qo::f6_workspace_bytes(M, N, K);
 }

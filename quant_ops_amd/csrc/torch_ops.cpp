@@ -109,19 +109,20 @@ at::Tensor int4_matmul_impl(const at::Tensor& a, const at::Tensor& b, const at::
   if (KP == 1) bsp = 1;     // a single packed row: either stride works
   if (N == 1) bsn = 1;
   const int64_t lda = M > 0 ? A.stride(0) : KP;
+  at::Tensor bv;
   if (bias.has_value()) {
     TORCH_CHECK(bias->is_cuda() && bias->numel() == N, "bias must be a GPU tensor of N elements");
     // the reference adds bias.to(output dtype) to the output
-    at::Tensor bv = bias->to(out_dtype).contiguous();
-    check_status(qo_int4_gemm_bias(A.data_ptr<int32_t>(), lda, B.data_ptr<int32_t>(), bsp, bsn, sa.data_ptr(), sad,
-                                   sb.data_ptr(), sbd, bv.data_ptr(), out.data_ptr(), od, N, M, N, K,
-                                   current_stream(a)),
-                 "int4_matmul_bias");
-    return out;
+    bv = bias->to(out_dtype).contiguous();
   }
-  check_status(qo_int4_gemm(A.data_ptr<int32_t>(), lda, B.data_ptr<int32_t>(), bsp, bsn, sa.data_ptr(), sad,
-                            sb.data_ptr(), sbd, out.data_ptr(), od, N, M, N, K, current_stream(a)),
-               "int4_matmul");
+  // workspace of the FP6 route for the large shapes (the caching allocator's
+  // blocks are 512-byte aligned)
+  const int64_t ws_bytes = qo_int4_gemm_workspace_size(M, N, K, od);
+  at::Tensor ws = ws_bytes > 0 ? at::empty({ws_bytes}, a.options().dtype(at::kByte)) : at::Tensor();
+  check_status(qo_int4_gemm_ws(A.data_ptr<int32_t>(), lda, B.data_ptr<int32_t>(), bsp, bsn, sa.data_ptr(), sad,
+                               sb.data_ptr(), sbd, bv.defined() ? bv.data_ptr() : nullptr, out.data_ptr(), od, N, M,
+                               N, K, ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(a)),
+               bias.has_value() ? "int4_matmul_bias" : "int4_matmul");
   return out;
 }
 

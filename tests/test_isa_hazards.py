@@ -115,9 +115,10 @@ def _instructions(dis):
 def test_no_valu_sgpr_hazard_before_lds_dma(tmp_path):
     texts = gfx950_disassembly(LIB, tmp_path)
     assert len(texts) >= 2
-    # the quantize and the GEMM sources both copy through LDS-DMA
+    # the quantize and both GEMM sources copy through LDS-DMA
     with_dma = [t for t in texts if "global_load_lds" in t]
-    assert any("fq_few2_kernel" in t for t in with_dma) and any("gemm_i4_pp2" in t for t in with_dma)
+    for kernel in ("fq_few2_kernel", "gemm_i4_pp2", "gemm_f6_pp2"):
+        assert any(kernel in t for t in with_dma), kernel
     for dis in with_dma:
         lines = _instructions(dis)
         n_dma = sum(1 for x in lines if x.startswith("global_load_lds"))
