@@ -3,9 +3,12 @@
 
 Prints ONE JSON line. The headline (``value``) is BASELINE config 4, the W4A4
 GEMM 4096 x 14336 x 4096 the north-star target names: int32-packed int4 codes
-times int32-packed int4 codes on the i8 MFMA with int32 accumulation, fp16
-per-token and per-channel scales, fp16 output. One step is one GEMM call;
-``value`` is 2 M N K per step over the time of exactly ``--steps`` steps.
+times int32-packed int4 codes, fp16 per-token and per-channel scales, fp16
+output. One step is one GEMM call as the torch operator makes it (with a
+workspace: the operands converted to exact FP6 e2m3 values, then the FP6
+matrix-core GEMM; the int32 route of the same call is timed beside it);
+``value`` is 2 M N K per step over the time of exactly ``--steps`` steps, and
+the roofline is the FP6 GEMM kernel's own rate against the dense FP6 peak.
 
 Every BASELINE config has an object in ``lines`` with its own ``roofline``
 (achieved rate of the config's dominant kernel against the MI355X peak of its
@@ -50,6 +53,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, TOP/s
+FP6_PEAK_TOPS = 10100.0        # MI355X dense FP6 / FP4 MFMA, TFLOP/s
 MALL_BYTES = 256 * 2**20
 ROTATION_CAP_BYTES = 48 * 2**30
 METRIC = "quantize GB/s + W4A4 GEMM TOPS on 1 MI355X; % of HBM / i8-MFMA roofline"
@@ -130,6 +134,14 @@ def _mfma(tops):
             "frac": tops / INT8_PEAK_TOPS}
 
 
+def _mfma_f6(tops):
+    """The FP6 route's GEMM kernel against the dense FP6 matrix-core peak (the
+    format it computes in); the int8 peak fraction beside it for comparison."""
+    return {"bound": "mfma", "achieved": tops, "peak": FP6_PEAK_TOPS, "unit": "TOP/s", "frac": tops / FP6_PEAK_TOPS,
+            "format": "fp6 e2m3 (int4 codes / 8, exact), fp32 accumulation",
+            "int8_peak": INT8_PEAK_TOPS, "frac_of_int8_peak": tops / INT8_PEAK_TOPS}
+
+
 # --------------------------------------------------------------------------- GPU measurements
 
 def bench_quant(torch, case, steps, warmup, dev):
@@ -166,6 +178,11 @@ def bench_quant(torch, case, steps, warmup, dev):
 
 
 def bench_gemm(torch, case, steps, warmup, dev):
+    """One step = one int4 GEMM call as the torch operator makes it: with a
+    workspace, so that products of more than 256 rows take the FP6 route (the
+    operand conversion, then the FP6 GEMM). Beside it, each of the two
+    kernels timed alone (the GEMM on a converted workspace gives the
+    roofline's kernel rate) and the integer route of the same call."""
     from quant_ops_amd import capi
 
     m, n, k = case.mnk
@@ -177,21 +194,45 @@ def bench_gemm(torch, case, steps, warmup, dev):
         [b0] + [b0.t().clone().t() for _ in range(nbuf - 1)]
     sa, sb = case.scale_a.to(dev), case.scale_b.to(dev)
     outs = [torch.empty((m, n), dtype=case.out_dtype, device=dev) for _ in range(nbuf)]
+    ws_bytes = capi.gemm_workspace_size(m, n, k, case.out_dtype)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
 
     def launch(i):
         j = i % nbuf
-        capi.int4_gemm(As[j], Bs[j], sa, sb, out=outs[j])
+        capi.int4_gemm(As[j], Bs[j], sa, sb, out=outs[j], workspace=ws)
 
     gpu_ms, wall = _time_graph(torch, launch, steps, warmup)
     per_step_s = gpu_ms / 1e3 / steps
     tops = case.ops() / per_step_s / 1e12
     out = {
         "workload": case.name, "M": m, "N": n, "K": k, "b_layout": "KN" if b0.is_contiguous() else "W.t()",
-        "out_dtype": str(case.out_dtype).replace("torch.", ""), "ops_per_step": case.ops(),
-        "bytes_per_step": per_set, "buffers_rotated": nbuf, "us_per_step": per_step_s * 1e6, "TOPS": tops,
-        "GBps": per_set / per_step_s / 1e9, "wall_s": wall, "roofline": _mfma(tops),
+        "out_dtype": str(case.out_dtype).replace("torch.", ""), "route": "fp6" if ws_bytes else "int8",
+        "ops_per_step": case.ops(), "bytes_per_step": per_set, "buffers_rotated": nbuf,
+        "us_per_step": per_step_s * 1e6, "TOPS": tops, "GBps": per_set / per_step_s / 1e9, "wall_s": wall,
+        "roofline": _mfma(tops),
     }
-    del As, Bs, outs
+    if ws_bytes:
+        def convert(i):
+            capi.f6_prepare(ws, m, n, k, a=As[i % nbuf], b=Bs[i % nbuf])
+
+        def f6_gemm(i):
+            capi.f6_run(ws, m, n, k, sa, sb, out_dtype=case.out_dtype, out=outs[i % nbuf])
+
+        def int8_route(i):
+            capi.int4_gemm(As[i % nbuf], Bs[i % nbuf], sa, sb, out=outs[i % nbuf])
+
+        ms_c, _ = _time_graph(torch, convert, steps, warmup)
+        ms_g, _ = _time_graph(torch, f6_gemm, steps, warmup)      # on the last set's converted operands
+        ms_i, _ = _time_graph(torch, int8_route, steps, warmup)
+        t_c, t_g, t_i = (ms / 1e3 / steps for ms in (ms_c, ms_g, ms_i))
+        conv_bytes = (m + n) * k // 2 + (m + n) * k * 3 // 4
+        out.update({
+            "convert_us": t_c * 1e6, "convert_bytes": conv_bytes, "convert_GBps": conv_bytes / t_c / 1e9,
+            "f6_gemm_kernel_us": t_g * 1e6, "f6_gemm_kernel_TOPS": case.ops() / t_g / 1e12,
+            "int8_route_us": t_i * 1e6, "int8_route_TOPS": case.ops() / t_i / 1e12,
+            "roofline": _mfma_f6(case.ops() / t_g / 1e12),
+        })
+    del As, Bs, outs, ws
     torch.cuda.empty_cache()
     return out
 
@@ -478,7 +519,8 @@ def cpu_dequant(torch, budget_s):
 
 # Kernel of each benched workload, as rocprofv3 names it (a substring of the demangled name).
 KERNEL_OF = {
-    "gemm_cfg4": "gemm_i4_pp2<256, 224, false, qo::OutF16>",
+    "gemm_cfg4": "gemm_f6_pp2<256, 224, qo::OutF16>",
+    "convert_cfg4": "f6_convert_kernel",
     "quantize_cfg2": "fq_wave_kernel<qo::F16T, 4, 2, true>",
     "quantize_cfg3": "fq_few2_kernel<qo::BF16T, 7, true, true, true>",
     "gemm_cfg5_T16": "gemm_i4_skinny_nk",
@@ -503,7 +545,7 @@ def pmc_pass(torch, dev):
     sa, sb = case.scale_a.to(dev), case.scale_b.to(dev)
     for _ in range(4):
         out = torch.empty(case.mnk[:2], dtype=case.out_dtype, device=dev)
-        capi.int4_gemm(a.clone(), b.clone(), sa, sb, out=out)
+        capi.int4_gemm(a.clone(), b.clone(), sa, sb, out=out, workspace=True)
         torch.cuda.synchronize()
     del a, b, out
     for case in (wl.quant_cfg2(), wl.quant_cfg3()):
@@ -619,11 +661,15 @@ def _lin_q_bytes(t):
     return t * LIN_K * 2 + t * LIN_K // 2 + t * 4 + 2 * (LIN_M ** 2 + LIN_NT ** 2)
 
 
+F6_CONVERT_BYTES_CFG4 = (4096 + 14336) * 4096 * 5 // 4   # int4 in, FP6 out
+
 # Workloads in the order the default bench run dispatches them (one segment of
 # launches each, in order of first dispatch; a config 5 step interleaves its
 # two kernels, which then form one segment each).
 BENCH_SEGMENTS = [
-    ("gemm cfg4", None, 481036337152), ("quantize cfg2", 20996096, None),
+    ("gemm cfg4 step: convert", F6_CONVERT_BYTES_CFG4, None), ("gemm cfg4 step: f6 gemm", None, 481036337152),
+    ("gemm cfg4 convert alone", F6_CONVERT_BYTES_CFG4, None), ("gemm cfg4 f6 gemm alone", None, 481036337152),
+    ("gemm cfg4 int8 route", None, 481036337152), ("quantize cfg2", 20996096, None),
     ("copy probe cfg2 bytes", 20996096, None), ("quantize cfg3", 293691904, None),
     ("cfg5 T=16 quantize", _lin_q_bytes(16), None), ("cfg5 T=16 gemm", None, 2 * 16 * LIN_N * LIN_K),
     ("cfg5 T=16 step quant", _lin_q_bytes(16), None), ("cfg5 T=16 step gemm", None, 2 * 16 * LIN_N * LIN_K),
@@ -851,7 +897,9 @@ def power(torch, dev, seconds=2.0):
     def gemm(case):
         a, b, sa, sb = case.a.to(dev), case.b.to(dev), case.scale_a.to(dev), case.scale_b.to(dev)
         out = torch.empty(case.mnk[:2], dtype=case.out_dtype, device=dev)
-        return lambda: capi.int4_gemm(a, b, sa, sb, out_dtype=case.out_dtype, out=out)
+        m, n, k = case.mnk
+        ws = torch.empty(max(1, capi.gemm_workspace_size(m, n, k, case.out_dtype)), dtype=torch.uint8, device=dev)
+        return lambda: capi.int4_gemm(a, b, sa, sb, out_dtype=case.out_dtype, out=out, workspace=ws)
 
     def quant(case):
         x, L, R = case.x.to(dev), case.left.to(dev), case.right.to(dev)
@@ -967,7 +1015,9 @@ def main():
     _log("headline: config 4 GEMM")
     head = bench_gemm(torch, wl.gemm_cfg4(), steps, warmup, dev)
     head["roofline"]["traffic"] = _traffic_from_profiles("gemm_cfg4")
-    _log(f"config 4: {head['us_per_step']:.1f} us/step, {head['TOPS']:.0f} TOP/s")
+    _log(f"config 4: {head['us_per_step']:.1f} us/step, {head['TOPS']:.0f} TOP/s"
+         + (f" (convert {head['convert_us']:.1f} us, FP6 GEMM {head['f6_gemm_kernel_us']:.1f} us; "
+            f"int32 route {head['int8_route_us']:.1f} us)" if head.get("route") == "fp6" else ""))
     lines = {"gemm_cfg4": head}
     if not args.no_secondary:
         _log("config 2 quantize")
@@ -1020,13 +1070,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i8",
+        "dtype": "fp6",
         "data": "synthetic: seeded uniform int4 codes in [-8, 7] packed 8 per int32, fp16 scales U(0.01, 0.1) per "
                 "token and U(0.001, 0.01) per channel; quantize lines: seeded N(0,1) activations with outlier "
                 "channels, orthogonal transforms from QR of seeded Gaussians",
         "config": {
             "workload": "BASELINE config 4: int4_matmul A [4096, 4096/8] x B [4096/8, 14336] int32-packed int4, "
-                        "int32 accumulate on the i8 MFMA, fp16 out (one step = one GEMM call)",
+                        "fp16 out; one step = one GEMM call as the torch operator makes it: both operands "
+                        "converted to FP6 e2m3 (q / 8, exact), then the f8f6f4 MFMA with fp32 accumulation "
+                        "(exact integer sums, outputs bit-identical to the int32 path)",
             "M": 4096, "N": 14336, "K": 4096,
         },
         "roofline": head["roofline"],
