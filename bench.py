@@ -706,6 +706,9 @@ def ceilings_summary(trace_csv):
         if short.startswith("probe_mfma_i8"):
             waves = grid // 64   # the data probe's rows mix its zero and random runs; bench.py's log splits them
             rate = f"{2 * 16 * 16 * 64 * 8 * 4096 * waves / (med * 1e-6) / 1e12:.0f} TOP/s (median)"
+        elif short.startswith("probe_mfma_f6"):
+            waves = grid // 64   # rows mix the zero, int4-code and random-field runs; bench.py's log splits them
+            rate = f"{2 * 16 * 16 * 128 * 8 * 4096 * waves / (med * 1e-6) / 1e12:.0f} TOP/s (median)"
         elif short.startswith("probe_stream"):
             rate = f"{2048 * 4096 * 2 * 5 / 4 / (med * 1e-6) / 1e9:.0f} GB/s (median)"
         print(f"{short:28s} {block:5d} {grid:9d} {len(v):6d} {avg:9.2f} {med:9.2f}  {rate}")
@@ -751,7 +754,7 @@ def trace_summary(trace_csv, tail=None):
         name, nbytes, ops = BENCH_SEGMENTS[i] if labelled else (f"segment {i}", None, None)
         gbs = f"{nbytes / avg / 1e3:7.0f}" if nbytes else f"{'':7s}"
         tops = f"{ops / avg / 1e6:7.0f}" if ops else f"{'':7s}"
-        kname = s["key"][0].split("(")[0].replace("void ", "")[:110]
+        kname = s["key"][0].replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")[:110]
         lines.append(f"{name:24s} {len(d):5d} {avg:9.2f} {statistics.median(d) / 1e3:9.2f} {min(d) / 1e3:9.2f} "
                      f"{max(d) / 1e3:9.2f} {gbs} {tops}  {kname} [{s['key'][1]} x {s['key'][2]}]")
     print("\n".join(lines))
@@ -770,6 +773,27 @@ def _traffic_from_profiles(kernel_key):
 
 
 # --------------------------------------------------------------------------- ceilings
+
+def _f6_probe_operands(torch, g, int4):
+    """16 x 1024 FP6 fragments of 32 bytes (24 used): 32 six-bit fields per
+    lane, either int4 codes as the FP6 route encodes them (sign in bit 5,
+    |q| <= 8 below it) or random fields."""
+    n = 16 * 1024
+    if int4:
+        q = torch.randint(-8, 8, (n, 32), generator=g)
+        fields = torch.where(q < 0, 32, 0) | q.abs()
+    else:
+        fields = torch.randint(0, 64, (n, 32), generator=g)
+    words = torch.zeros(n, 8, dtype=torch.int64)
+    for j in range(32):
+        bit = 6 * j
+        w, o = divmod(bit, 32)
+        words[:, w] |= (fields[:, j] << o) & 0xFFFFFFFF
+        if o > 26:
+            words[:, w + 1] |= fields[:, j] >> (32 - o)
+    words = torch.where(words >= 2**31, words - 2**32, words)
+    return words.to(torch.int32).reshape(-1)
+
 
 def ceilings(torch, steps, warmup, dev):
     """Microbenchmarks of the ceilings the kernels are compared with
@@ -826,6 +850,28 @@ def ceilings(torch, steps, warmup, dev):
                  f"{ops / (us * 1e-6) / 1e12:.0f} TOP/s")
     out["mfma_i8_operands_from_memory"] = data
 
+    # the FP6 matrix cores on FP6 operands: zeros, int4 codes as the FP6 route
+    # stores them (q / 8: sign-magnitude, 6-bit fields), random 6-bit fields
+    lib.qo_probe_mfma_f6_data.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp]
+    fsink = torch.empty(cus * 512, dtype=torch.float32, device=dev)
+    f6_srcs = {"zero": torch.zeros(16 * 1024 * 8, dtype=torch.int32, device=dev),
+               "int4_codes": _f6_probe_operands(torch, g, True).to(dev),
+               "random_fields": _f6_probe_operands(torch, g, False).to(dev)}
+    f6 = {}
+    for name, src in f6_srcs.items():
+        for kv in (0, 2):
+            def launch(i, kv=kv, src=src):
+                assert lib.qo_probe_mfma_f6_data(kv, cus, iters, ctypes.c_void_p(src.data_ptr()),
+                                                 ctypes.c_void_p(fsink.data_ptr()), ctypes.c_void_p(cycles.data_ptr()),
+                                                 stream()) == 0
+            ms, _ = _time_graph(torch, launch, steps, warmup)
+            us = ms / steps * 1e3
+            ops = 2 * 16 * 16 * 128 * 8 * iters * 8 * cus
+            f6[f"{name}_valu_per_mfma_{kv}"] = {"us_per_launch": us, "TOPS": ops / (us * 1e-6) / 1e12}
+            _log(f"ceiling: FP6 MFMA on {name} operands, two waves per SIMD, {kv} VALU per MFMA: "
+                 f"{ops / (us * 1e-6) / 1e12:.0f} TOP/s")
+    out["mfma_f6_operands_from_memory"] = f6
+
     def launch_empty(i):
         assert lib.qo_probe_empty(stream()) == 0
     ms, _ = _time_graph(torch, launch_empty, steps, warmup)
@@ -868,8 +914,10 @@ def _smi_sample():
 
 def power(torch, dev, seconds=2.0):
     """Board power and shader clock while each workload runs back to back:
-    the MFMA probe on zero, widened-int4 and random operands, the config 4 and
-    config 5 (T = 4096) GEMMs and the config 2 and config 3 quantizes. Each
+    the int8 MFMA probe on zero, widened-int4 and random operands, the FP6 MFMA
+    probe on zero and int4-code operands, the config 4 and config 5 (T = 4096)
+    GEMMs as the torch operator runs them and the config 2 and config 3
+    quantizes. Each
     runs in a loop on a thread for ``seconds`` before three samples are taken
     (medians reported); one JSON line."""
     import ctypes
@@ -888,6 +936,16 @@ def power(torch, dev, seconds=2.0):
     rnd = torch.randint(-2**31, 2**31 - 1, (16 * 1024 * 4,), generator=g, dtype=torch.int64).to(torch.int32)
     srcs = {"zero": torch.zeros_like(rnd).to(dev), "widened_int4": (rnd & int(0xF0F0F0F0 - 2**32)).to(dev),
             "random": rnd.to(dev)}
+
+    lib.qo_probe_mfma_f6_data.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp]
+    fsink = torch.empty(cus * 512, dtype=torch.float32, device=dev)
+    f6_srcs = {"zero": torch.zeros(16 * 1024 * 8, dtype=torch.int32, device=dev),
+               "int4_codes": _f6_probe_operands(torch, g, True).to(dev)}
+
+    def probe_f6(src, kv):
+        return lambda: lib.qo_probe_mfma_f6_data(kv, cus, 8192, ctypes.c_void_p(src.data_ptr()),
+                                                 ctypes.c_void_p(fsink.data_ptr()),
+                                                 ctypes.c_void_p(cycles.data_ptr()), None)
 
     def probe(src, kv):
         return lambda: lib.qo_probe_mfma_i8_data(kv, cus, 16384, ctypes.c_void_p(src.data_ptr()),
@@ -909,7 +967,10 @@ def power(torch, dev, seconds=2.0):
     for name in srcs:
         for kv in (0, 2):
             work.append((f"mfma_i8 probe, {name} operands, {kv} VALU per MFMA", probe(srcs[name], kv)))
-    work += [("gemm cfg4", gemm(wl.gemm_cfg4())),
+    for name in f6_srcs:
+        for kv in (0, 2):
+            work.append((f"mfma_f6 probe, {name} operands, {kv} VALU per MFMA", probe_f6(f6_srcs[name], kv)))
+    work += [("gemm cfg4 (FP6 route: conversion + FP6 GEMM)", gemm(wl.gemm_cfg4())),
              ("gemm cfg5 T=4096", gemm(wl.gemm_case(4096, 4096, 14336, seed=2, b_transposed_view=True,
                                                     out_dtype=torch.bfloat16))),
              ("quantize cfg3", quant(wl.quant_cfg3())), ("quantize cfg2", quant(wl.quant_cfg2()))]

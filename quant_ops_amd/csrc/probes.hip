@@ -9,6 +9,10 @@
 //    random bytes (eight different A and B fragments per lane in turn, so the
 //    matrix cores switch like they do on real data; constant operands draw
 //    less power), and each wave's s_memtime ticks over the loop;
+//  * qo_probe_mfma_f6_data: the same for the FP6 matrix cores
+//    (v_mfma_scale_f32_16x16x128_f8f6f4, both operands FP6 e2m3, block
+//    scales 2^3 as the FP6 GEMM route uses them), 32-byte operands of which
+//    the instruction reads 24;
 //  * qo_probe_empty: an empty kernel (launch and wave start-up cost);
 //  * qo_probe_stream: a streaming kernel with the quantize's traffic shape,
 //    16 bytes read and 4 bytes written per lane per step (config 2 reads
@@ -19,6 +23,8 @@
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 // KV independent VALU instructions (one v_xor each, on four rotating
 // registers) after each MFMA; eight independent accumulator chains.
@@ -89,6 +95,45 @@ __global__ void __launch_bounds__(512) probe_mfma_i8_data(int iters, const v4i* 
   if (lane == 0) cycles[blockIdx.x * (blockDim.x >> 6) + wave] = t1 - t0;
 }
 
+// As probe_mfma_i8_data on FP6 operands: src holds 16 x 1024 fragments of 32
+// bytes (6 of 8 dwords used per lane).
+template <int KV>
+__global__ void __launch_bounds__(512) probe_mfma_f6_data(int iters, const v8i* __restrict__ src, float* out,
+                                                          unsigned long long* cycles) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const v8i* set = src + (size_t)((blockIdx.x * 8 + wave) % 16) * 1024;
+  v8i a[8], b[8];
+  v4f acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    a[j] = set[j * 64 + lane];
+    b[j] = set[512 + j * 64 + lane];
+    acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+  uint32_t x0 = t, x1 = 3 * t, x2 = 5 * t, x3 = 7 * t;
+  const uint32_t c = 0x5bd1e995u;
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[j], b[j], acc[j], 2, 2, 0, 130, 0, 130);
+#pragma unroll
+      for (int k = 0; k < KV; ++k) {
+        if (k % 4 == 0) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x0) : "v"(c));
+        if (k % 4 == 1) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x1) : "v"(c));
+        if (k % 4 == 2) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x2) : "v"(c));
+        if (k % 4 == 3) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x3) : "v"(c));
+      }
+    }
+  }
+  float s = (float)(x0 ^ x1 ^ x2 ^ x3);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  out[blockIdx.x * blockDim.x + t] = s;
+  if (lane == 0) cycles[blockIdx.x * (blockDim.x >> 6) + wave] = t1 - t0;
+}
+
 __global__ void probe_empty() {}
 
 // grid-stride: 16 bytes in, their four words XORed into 4 bytes out
@@ -127,6 +172,19 @@ extern "C" int qo_probe_mfma_i8_data(int kvalu, int blocks, int iters, const voi
     case 0: probe_mfma_i8_data<0><<<blocks, threads, 0, s>>>(iters, v, out, cycles); break;
     case 2: probe_mfma_i8_data<2><<<blocks, threads, 0, s>>>(iters, v, out, cycles); break;
     case 4: probe_mfma_i8_data<4><<<blocks, threads, 0, s>>>(iters, v, out, cycles); break;
+    default: return 1;
+  }
+  return (int)hipGetLastError();
+}
+
+// src: 16 x 1024 x 32 bytes; out: blocks x 512 floats; cycles: blocks x 8; 512 threads
+extern "C" int qo_probe_mfma_f6_data(int kvalu, int blocks, int iters, const void* src, float* out,
+                                     unsigned long long* cycles, void* stream) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const v8i* v = static_cast<const v8i*>(src);
+  switch (kvalu) {
+    case 0: probe_mfma_f6_data<0><<<blocks, 512, 0, s>>>(iters, v, out, cycles); break;
+    case 2: probe_mfma_f6_data<2><<<blocks, 512, 0, s>>>(iters, v, out, cycles); break;
     default: return 1;
   }
   return (int)hipGetLastError();
