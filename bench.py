@@ -271,20 +271,33 @@ def bench_linear(torch, tokens, steps, warmup, dev):
     scales = [torch.empty(tokens, dtype=torch.float32, device=dev) for _ in range(nbuf)]
     outs = [torch.empty(tokens, LIN_N, dtype=torch.bfloat16, device=dev) for _ in range(nbuf)]
 
+    # the GEMM's workspace, as the torch operator passes it (FP6 route above 256 tokens)
+    wsb = capi.gemm_workspace_size(tokens, LIN_N, LIN_K, torch.bfloat16)
+    work = torch.empty(wsb, dtype=torch.uint8, device=dev) if wsb else None
+
     def quant(j):
         capi.flatquant_quantize(xs[j], L, R, 0.9, True, out_codes=codes[j], out_scales=scales[j])
 
     def gemm(j):
-        capi.int4_gemm(codes[j], ws[j].t(), scales[j], sw, out=outs[j])
+        capi.int4_gemm(codes[j], ws[j].t(), scales[j], sw, out=outs[j], workspace=work)
 
     def step(j):
-        capi.w4a4_linear(xs[j], L, R, ws[j], sw, 0.9, out=outs[j], codes=codes[j], scales=scales[j])
+        capi.w4a4_linear(xs[j], L, R, ws[j], sw, 0.9, out=outs[j], codes=codes[j], scales=scales[j],
+                         workspace=work)
 
     for j in range(nbuf):      # codes of every set, for the GEMM timed alone
         quant(j)
     torch.cuda.synchronize()
     ms_q, _ = _time_graph(torch, lambda i: quant(i % nbuf), steps, warmup)
     ms_g, _ = _time_graph(torch, lambda i: gemm(i % nbuf), steps, warmup)
+    f6 = {}
+    if work is not None:      # the FP6 route's two launches timed apart
+        ms_c, _ = _time_graph(torch, lambda i: capi.f6_prepare(work, tokens, LIN_N, LIN_K, a=codes[i % nbuf],
+                                                                 b=ws[i % nbuf].t()), steps, warmup)
+        ms_r, _ = _time_graph(torch, lambda i: capi.f6_run(work, tokens, LIN_N, LIN_K, scales[i % nbuf], sw,
+                                                             out_dtype=torch.bfloat16, out=outs[i % nbuf]),
+                              steps, warmup)
+        f6 = {"convert_us": ms_c / steps * 1e3, "f6_gemm_kernel_us": ms_r / steps * 1e3}
     ms_s, wall = _time_graph(torch, lambda i: step(i % nbuf), steps, warmup)
     t_q, t_g, t_s = (ms / 1e3 / steps for ms in (ms_q, ms_g, ms_s))
     ops = 2 * tokens * LIN_N * LIN_K
@@ -299,7 +312,13 @@ def bench_linear(torch, tokens, steps, warmup, dev):
         "weight_GBps_gemm": w_bytes / t_g / 1e9, "weight_GBps_step": w_bytes / t_s / 1e9, "wall_s": wall,
     }
     # the dominant kernel: the GEMM; at 16 tokens it is a weight stream (HBM), at 4096 MFMA work
-    out["roofline"] = _hbm(gemm_gbs) if tokens <= 64 else _mfma(ops / t_g / 1e12)
+    out["route"] = "fp6" if work is not None else "int8"
+    out.update(f6)
+    if f6:
+        out["f6_gemm_kernel_TOPS"] = ops / (f6["f6_gemm_kernel_us"] * 1e-6) / 1e12
+        out["roofline"] = _mfma_f6(out["f6_gemm_kernel_TOPS"])
+    else:
+        out["roofline"] = _hbm(gemm_gbs) if tokens <= 64 else _mfma(ops / t_g / 1e12)
     del xs, ws, codes, scales, outs
     torch.cuda.empty_cache()
     return out
@@ -524,7 +543,7 @@ KERNEL_OF = {
     "quantize_cfg2": "fq_wave_kernel<qo::F16T, 4, 2, true>",
     "quantize_cfg3": "fq_few2_kernel<qo::BF16T, 7, true, true, true>",
     "gemm_cfg5_T16": "gemm_i4_skinny_nk",
-    "gemm_cfg5_T4096": "gemm_i4_pp2<256, 256, true, qo::OutBF16>",
+    "gemm_cfg5_T4096": "gemm_f6_pp2<256, 256, qo::OutBF16>",
 }
 COPY_PROBE_BYTES = 1 << 30      # float32 negation of 1 GiB: reads and writes exactly this many bytes
 COPY_PROBE_KERNEL = "neg_kernel"
@@ -568,7 +587,7 @@ def pmc_pass(torch, dev):
         w = w_h.to(dev)
         for _ in range(4):
             out = torch.empty(tokens, LIN_N, dtype=torch.bfloat16, device=dev)
-            capi.int4_gemm(codes.clone(), w.clone().t(), scales, sw, out=out)
+            capi.int4_gemm(codes.clone(), w.clone().t(), scales, sw, out=out, workspace=True)
             torch.cuda.synchronize()
         del w, out, codes, scales
     src = torch.randn(COPY_PROBE_BYTES // 4, device=dev)
@@ -662,6 +681,7 @@ def _lin_q_bytes(t):
 
 
 F6_CONVERT_BYTES_CFG4 = (4096 + 14336) * 4096 * 5 // 4   # int4 in, FP6 out
+F6_CONVERT_BYTES_CFG5 = (4096 + 4096) * 14336 * 5 // 4
 
 # Workloads in the order the default bench run dispatches them (one segment of
 # launches each, in order of first dispatch; a config 5 step interleaves its
@@ -673,8 +693,12 @@ BENCH_SEGMENTS = [
     ("copy probe cfg2 bytes", 20996096, None), ("quantize cfg3", 293691904, None),
     ("cfg5 T=16 quantize", _lin_q_bytes(16), None), ("cfg5 T=16 gemm", None, 2 * 16 * LIN_N * LIN_K),
     ("cfg5 T=16 step quant", _lin_q_bytes(16), None), ("cfg5 T=16 step gemm", None, 2 * 16 * LIN_N * LIN_K),
-    ("cfg5 T=4096 quantize", _lin_q_bytes(4096), None), ("cfg5 T=4096 gemm", None, 2 * 4096 * LIN_N * LIN_K),
-    ("cfg5 T=4096 step quant", _lin_q_bytes(4096), None), ("cfg5 T=4096 step gemm", None, 2 * 4096 * LIN_N * LIN_K),
+    ("cfg5 T=4096 quantize", _lin_q_bytes(4096), None),
+    ("cfg5 T=4096 gemm: convert", F6_CONVERT_BYTES_CFG5, None), ("cfg5 T=4096 gemm: f6 gemm", None, 2 * 4096 * LIN_N * LIN_K),
+    ("cfg5 T=4096 convert alone", F6_CONVERT_BYTES_CFG5, None),
+    ("cfg5 T=4096 f6 gemm alone", None, 2 * 4096 * LIN_N * LIN_K),
+    ("cfg5 T=4096 step quant", _lin_q_bytes(4096), None), ("cfg5 T=4096 step convert", F6_CONVERT_BYTES_CFG5, None),
+    ("cfg5 T=4096 step f6 gemm", None, 2 * 4096 * LIN_N * LIN_K),
     ("quantize cfg1", 128 * 4096 * 4 + 128 * 4096 + 128 * 4 + 2 * 64 * 64 * 4, None),
     ("pack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
     ("unpack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),

@@ -250,6 +250,23 @@ int qo_w4a4_linear(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
                    void* out, int64_t out_ld, void* stream);
 
 /*
+ * qo_w4a4_linear with a caller workspace for its GEMM, which then runs as
+ * qo_int4_gemm_ws: at more than 256 tokens (with qo_int4_gemm_workspace_size(
+ * tokens, out_features, M*N, x_dtype) bytes or more) on the FP6 route, the
+ * codes and the weight converted into the workspace first. Same results as
+ * qo_w4a4_linear bit for bit; the torch operator w4a4_linear passes one.
+ * workspace may be NULL (then exactly qo_w4a4_linear).
+ *
+ * Errors: those of qo_w4a4_linear.
+ */
+int qo_w4a4_linear_ws(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
+                      const void* left, const void* right, int M, int N, float clip_ratio,
+                      const int32_t* weight, int64_t weight_ld, int64_t out_features,
+                      const void* weight_scale, int weight_scale_dtype, const void* bias,
+                      int32_t* codes, float* act_scales, void* out, int64_t out_ld,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * qo_w4a4_linear without caller buffers for the activation codes and scales,
  * for callers that cannot allocate device memory (HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). No counterpart in the

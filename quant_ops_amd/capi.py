@@ -21,7 +21,7 @@ STATUS = {0: "QO_OK", 1: "QO_ERR_NULL_POINTER", 2: "QO_ERR_SHAPE", 3: "QO_ERR_DT
 # Every symbol the header declares; the CPU tests check they are all exported.
 EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_set_kernel_routing", "qo_flatquant_quantize",
             "qo_int4_gemm", "qo_int4_gemm_bias", "qo_int4_gemm_ws", "qo_int4_gemm_workspace_size", "qo_int4_gemm_f6_workspace_bytes",
-            "qo_int4_gemm_f6_prepare", "qo_int4_gemm_f6_run", "qo_w4a4_linear", "qo_w4a4_linear_noalloc", "qo_dequantize_int4",
+            "qo_int4_gemm_f6_prepare", "qo_int4_gemm_f6_run", "qo_w4a4_linear", "qo_w4a4_linear_ws", "qo_w4a4_linear_noalloc", "qo_dequantize_int4",
             "qo_pack_int4_to_int32", "qo_unpack_int32_to_int4", "qo_transpose_int32")
 
 # QO_ROUTE_* bits of qo_set_kernel_routing (include/quant_ops_hip.h)
@@ -82,6 +82,9 @@ def lib():
     L.qo_w4a4_linear.restype = c_int
     L.qo_w4a4_linear.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_vp, c_i64, c_i64,
                                  c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]
+    L.qo_w4a4_linear_ws.restype = c_int
+    L.qo_w4a4_linear_ws.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_vp, c_i64, c_i64,
+                                    c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp]
     L.qo_w4a4_linear_noalloc.restype = c_int
     L.qo_w4a4_linear_noalloc.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_vp, c_i64,
                                          c_i64, c_vp, c_int, c_vp, c_vp, c_i64, c_vp]
@@ -237,11 +240,12 @@ def f6_run(workspace, m, n, k, scale_a, scale_b, out_dtype=torch.float16, out=No
 
 
 def w4a4_linear(x, left, right, weight, weight_scale, clip_ratio=1.0, bias=None, out=None, codes=None,
-                scales=None, stream=None):
+                scales=None, stream=None, workspace=None):
     """Call ``qo_w4a4_linear``: x [T, M*N] (float32 / float16 / bfloat16), the packed
     weight int32 [out, M*N/8] (rows may be strided), weight_scale [out], optional
     bias [out] (converted to x's dtype). Returns (out [T, out] in x's dtype, packed
-    codes [T, M*N/8], float32 scales [T])."""
+    codes [T, M*N/8], float32 scales [T]). With ``workspace`` (a uint8 device
+    tensor, or True to allocate gemm_workspace_size bytes) ``qo_w4a4_linear_ws``."""
     t, f = x.shape
     if x.stride(1) != 1:
         x = x.contiguous()
@@ -259,14 +263,21 @@ def w4a4_linear(x, left, right, weight, weight_scale, clip_ratio=1.0, bias=None,
         out = torch.empty((t, no), dtype=x.dtype, device=x.device)
     if bias is not None:
         bias = bias.to(x.dtype).contiguous()
-    _check(lib().qo_w4a4_linear(
-        ctypes.c_void_p(x.data_ptr()), _TORCH_CODE[x.dtype], t, x.stride(0) if t else f,
-        ctypes.c_void_p(left.data_ptr()), ctypes.c_void_p(right.data_ptr()), m, n, float(clip_ratio),
-        ctypes.c_void_p(weight.data_ptr()), _ld(weight), no,
-        ctypes.c_void_p(weight_scale.data_ptr()), _TORCH_CODE[weight_scale.dtype],
-        ctypes.c_void_p(bias.data_ptr() if bias is not None else None),
-        ctypes.c_void_p(codes.data_ptr()), ctypes.c_void_p(scales.data_ptr()),
-        ctypes.c_void_p(out.data_ptr()), out.stride(0) if t else no, _stream(stream)))
+    args = (ctypes.c_void_p(x.data_ptr()), _TORCH_CODE[x.dtype], t, x.stride(0) if t else f,
+            ctypes.c_void_p(left.data_ptr()), ctypes.c_void_p(right.data_ptr()), m, n, float(clip_ratio),
+            ctypes.c_void_p(weight.data_ptr()), _ld(weight), no,
+            ctypes.c_void_p(weight_scale.data_ptr()), _TORCH_CODE[weight_scale.dtype],
+            ctypes.c_void_p(bias.data_ptr() if bias is not None else None),
+            ctypes.c_void_p(codes.data_ptr()), ctypes.c_void_p(scales.data_ptr()),
+            ctypes.c_void_p(out.data_ptr()), out.stride(0) if t else no)
+    if workspace is None:
+        _check(lib().qo_w4a4_linear(*args, _stream(stream)))
+    else:
+        if workspace is True:
+            workspace = torch.empty(max(1, gemm_workspace_size(t, no, f, x.dtype)), dtype=torch.uint8,
+                                    device=x.device)
+        _check(lib().qo_w4a4_linear_ws(*args, ctypes.c_void_p(workspace.data_ptr()), workspace.numel(),
+                                       _stream(stream)))
     return out, codes, scales
 
 

@@ -45,7 +45,6 @@ namespace {
 constexpr int kF6Pair = 3072;   // bytes of one fragment pair (32 rows x 128 codes)
 
 typedef int v8i __attribute__((ext_vector_type(8)));
-typedef int v12i __attribute__((ext_vector_type(12)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 // Eight offset codes (nibble i = q_i + 8) -> the FP6 e2m3 codes of q_i / 8,

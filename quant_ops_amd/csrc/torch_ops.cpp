@@ -185,10 +185,14 @@ at::Tensor w4a4_linear(const at::Tensor& x, const at::Tensor& left_trans, const 
   at::Tensor codes = at::empty({T, F / 8}, x.options().dtype(at::kInt));
   at::Tensor scales = at::empty({T}, x.options().dtype(at::kFloat));
   at::Tensor out = at::empty({T, NO}, x.options());
-  check_status(qo_w4a4_linear(X.data_ptr(), code, T, T > 0 ? X.stride(0) : F, L.data_ptr(), R.data_ptr(), (int)M,
-                              (int)N, (float)clip_ratio, W.data_ptr<int32_t>(), NO > 0 ? W.stride(0) : F / 8, NO,
-                              sw.data_ptr(), swd, bv.defined() ? bv.data_ptr() : nullptr, codes.data_ptr<int32_t>(),
-                              scales.data_ptr<float>(), out.data_ptr(), NO, current_stream(x)),
+  // the GEMM's FP6 route at large token counts (0 bytes: not taken)
+  const int64_t ws_bytes = qo_int4_gemm_workspace_size(T, NO, F, code);
+  at::Tensor ws = ws_bytes > 0 ? at::empty({ws_bytes}, x.options().dtype(at::kByte)) : at::Tensor();
+  check_status(qo_w4a4_linear_ws(X.data_ptr(), code, T, T > 0 ? X.stride(0) : F, L.data_ptr(), R.data_ptr(), (int)M,
+                                 (int)N, (float)clip_ratio, W.data_ptr<int32_t>(), NO > 0 ? W.stride(0) : F / 8, NO,
+                                 sw.data_ptr(), swd, bv.defined() ? bv.data_ptr() : nullptr,
+                                 codes.data_ptr<int32_t>(), scales.data_ptr<float>(), out.data_ptr(), NO,
+                                 ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, current_stream(x)),
                "w4a4_linear");
   return out;
 }

@@ -26,7 +26,8 @@ static int inner_failed(const char* fn, int status) {
 static int linear_run(const char* fn, const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
                       const void* right, int M, int N, float clip_ratio, const int32_t* weight, int64_t weight_ld,
                       int64_t out_features, const void* weight_scale, int weight_scale_dtype, const void* bias,
-                      int32_t* codes, float* act_scales, void* out, int64_t out_ld, void* stream) {
+                      int32_t* codes, float* act_scales, void* out, int64_t out_ld, void* stream,
+                      void* workspace = nullptr, int64_t workspace_bytes = 0) {
   using namespace qo;
   if (tokens < 0 || M < 1 || N < 1 || out_features < 1) {
     qo_set_error("%s: invalid sizes tokens=%lld M=%d N=%d out_features=%lld", fn, (long long)tokens, M, N,
@@ -72,11 +73,17 @@ static int linear_run(const char* fn, const void* x, int x_dtype, int64_t tokens
   const int q = flatquant_quantize(x, x_dtype, tokens, x_ld, left, right, M, N, clip_ratio, 1, codes, act_scales,
                                    stream, ahead);
   if (q != QO_OK) return inner_failed(fn, q);
-  const int g = bias ? qo_int4_gemm_bias(codes, features / 8, weight, 1, weight_ld, act_scales, QO_DTYPE_F32,
-                                         weight_scale, weight_scale_dtype, bias, out, x_dtype, out_ld, tokens,
-                                         out_features, features, stream)
-                     : qo_int4_gemm(codes, features / 8, weight, 1, weight_ld, act_scales, QO_DTYPE_F32, weight_scale,
-                                    weight_scale_dtype, out, x_dtype, out_ld, tokens, out_features, features, stream);
+  int g;
+  if (workspace)   // the FP6 route where the workspace and the shape allow it
+    g = qo_int4_gemm_ws(codes, features / 8, weight, 1, weight_ld, act_scales, QO_DTYPE_F32, weight_scale,
+                        weight_scale_dtype, bias, out, x_dtype, out_ld, tokens, out_features, features, workspace,
+                        workspace_bytes, stream);
+  else if (bias)
+    g = qo_int4_gemm_bias(codes, features / 8, weight, 1, weight_ld, act_scales, QO_DTYPE_F32, weight_scale,
+                          weight_scale_dtype, bias, out, x_dtype, out_ld, tokens, out_features, features, stream);
+  else
+    g = qo_int4_gemm(codes, features / 8, weight, 1, weight_ld, act_scales, QO_DTYPE_F32, weight_scale,
+                     weight_scale_dtype, out, x_dtype, out_ld, tokens, out_features, features, stream);
   return g == QO_OK ? g : inner_failed(fn, g);
 }
 
@@ -87,6 +94,16 @@ extern "C" int qo_w4a4_linear(const void* x, int x_dtype, int64_t tokens, int64_
                               int64_t out_ld, void* stream) {
   return linear_run("qo_w4a4_linear", x, x_dtype, tokens, x_ld, left, right, M, N, clip_ratio, weight, weight_ld,
                     out_features, weight_scale, weight_scale_dtype, bias, codes, act_scales, out, out_ld, stream);
+}
+
+extern "C" int qo_w4a4_linear_ws(const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
+                                 const void* right, int M, int N, float clip_ratio, const int32_t* weight,
+                                 int64_t weight_ld, int64_t out_features, const void* weight_scale,
+                                 int weight_scale_dtype, const void* bias, int32_t* codes, float* act_scales,
+                                 void* out, int64_t out_ld, void* workspace, int64_t workspace_bytes, void* stream) {
+  return linear_run("qo_w4a4_linear_ws", x, x_dtype, tokens, x_ld, left, right, M, N, clip_ratio, weight, weight_ld,
+                    out_features, weight_scale, weight_scale_dtype, bias, codes, act_scales, out, out_ld, stream,
+                    workspace, workspace_bytes);
 }
 
 // ---------------------------------------------------------------------------

@@ -192,3 +192,37 @@ def test_graph_replay(gpu):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.cpu(), ref), f"replay {r}"
+
+
+@pytest.mark.parametrize("tokens,out_f", [(300, 272), (1024, 4096)])
+def test_linear_workspace_entry_point(gpu, tokens, out_f):
+    """qo_w4a4_linear_ws (the GEMM on the FP6 route above 256 tokens) equals
+    qo_w4a4_linear bit for bit, and its GEMM output equals the oracle's
+    product of the codes the call returned."""
+    from test_gpu_parity import _linear_inputs, _linear_ref
+
+    m, n, dtype = 112, 128, torch.bfloat16
+    x, L, R, w, sw, bias = _linear_inputs(tokens, m, n, out_f, dtype, 900 + tokens)
+    args = (x.to(gpu), L.to(gpu), R.to(gpu), w.to(gpu), sw.to(gpu), 0.9, bias.to(gpu))
+    _say(f"linear ws T={tokens} {m}x{n} -> {out_f}")
+    assert capi.gemm_workspace_size(tokens, out_f, m * n, dtype) > 0
+    y_ws, q_ws, s_ws = capi.w4a4_linear(*args, workspace=True)
+    y, q, s = capi.w4a4_linear(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(q_ws, q) and torch.equal(s_ws, s)
+    assert torch.equal(y_ws, y)
+    assert torch.equal(y_ws.cpu(), _linear_ref(q_ws.cpu(), s_ws.cpu(), w, sw, bias, dtype))
+
+
+def test_linear_torch_operator_large_tokens(gpu):
+    """The torch operator w4a4_linear passes a workspace: at 512 tokens its
+    output equals the entry point without one."""
+    m, n, out_f, dtype = 64, 128, 1024, torch.float16
+    from test_gpu_parity import _linear_inputs
+
+    x, L, R, w, sw, bias = _linear_inputs(512, m, n, out_f, dtype, 950)
+    args = (x.to(gpu), L.to(gpu), R.to(gpu), w.to(gpu), sw.to(gpu))
+    y_op = torch.ops.quant_ops.w4a4_linear(*args, 0.9, bias.to(gpu))
+    y, _, _ = capi.w4a4_linear(*args, 0.9, bias.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(y_op, y)
