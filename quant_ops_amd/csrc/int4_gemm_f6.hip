@@ -75,62 +75,82 @@ struct F6Job {
   int blocks;              // workgroups of this job
 };
 
-// 256 threads, one 192-bit lane value (32 codes) each. Row-major sources: a
-// workgroup covers 4 consecutive k-blocks of one 16-row group, a wave one
-// fragment (reads: 16 rows x 64 contiguous bytes). Column sources
-// ([K/8, N]): a workgroup covers 64 consecutive rows and one k-block, wave g
-// the codes 32 g .. 32 g + 31 (reads: 256 contiguous bytes per packed row).
-// Every row group of the last pair is written (zeros past R).
+// The 192-bit lane value of four packed words (codes 8 t + i in word t):
+// three 64-bit pieces.
+struct F6Lane {
+  uint64_t u0, u1, u2;
+};
+__device__ inline F6Lane f6_lane(const uint32_t (&w)[4]) {
+  const uint64_t d0 = f6_codes8(w[0]), d1 = f6_codes8(w[1]), d2 = f6_codes8(w[2]), d3 = f6_codes8(w[3]);
+  return F6Lane{d0 | (d1 << 48), (d1 >> 16) | (d2 << 32), (d2 >> 32) | (d3 << 16)};
+}
+
+// 256 threads; a thread converts lane l = r % 16 + 16 g of one pair (32 rows,
+// one k-block): rows r and r + 16, 32 codes each, and writes the pair's three
+// whole 16-byte pieces of that lane. Row-major sources: a wave is one pair and
+// k-block (reads: 32 rows x 64 contiguous bytes), a workgroup 4 consecutive
+// k-blocks of that pair. Column sources ([K/8, N]): a wave is k-group g of
+// 4 consecutive pairs (reads: 4 x 2 runs of 64 bytes per packed row), a
+// workgroup the 4 k-groups of one k-block. Rows past R read as code 8
+// (q = 0), so every pair is written whole.
 __global__ void __launch_bounds__(256) f6_convert_kernel(F6Job j0, F6Job j1) {
   const bool second = (int)blockIdx.x >= j0.blocks;
   const F6Job j = second ? j1 : j0;
   const int b = second ? (int)blockIdx.x - j0.blocks : (int)blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  int r, kb, g;
+  const int pairs = (j.rows + 31) >> 5;
+  int pr, kb, g, rr;
   if (j.row_major) {
     const int kq = (j.kblocks + 3) >> 2;
     kb = (b % kq) * 4 + wave;
     if (kb >= j.kblocks) return;
-    r = (b / kq) * 16 + (lane & 15);
+    pr = b / kq;
+    rr = lane & 15;
     g = lane >> 4;
   } else {
-    const int rq = (j.rows + 63) >> 6;
-    kb = b / rq;
-    r = (b % rq) * 64 + lane;
+    const int pq = (pairs + 3) >> 2;
+    kb = b / pq;
+    pr = (b % pq) * 4 + (lane >> 4);
+    if (pr >= pairs) return;
+    rr = lane & 15;
     g = wave;
-    if (r >= ((j.rows + 31) & ~31)) return;   // past the last pair
   }
   const int p0 = kb * 16 + g * 4;
-  uint32_t w[4] = {0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};   // code 8: q = 0
-  if (r < j.rows) {
-    if (j.row_major) {
-      const int32_t* s = j.src + (int64_t)r * j.ld + p0;
+  const int r0 = pr * 32 + rr, r1 = r0 + 16;
+  uint32_t w0[4], w1[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) w0[t] = w1[t] = 0x88888888u;   // code 8: q = 0
+  if (j.row_major) {
+    auto row = [&](int r, uint32_t (&w)[4]) {
+      if (r >= j.rows) return;
+      const int32_t* src = j.src + (int64_t)r * j.ld + p0;
       if (j.vec && p0 + 4 <= j.kw) {
-        const v4i v = *reinterpret_cast<const v4i*>(s);
+        const v4i v = *reinterpret_cast<const v4i*>(src);
 #pragma unroll
         for (int t = 0; t < 4; ++t) w[t] = (uint32_t)v[t];
       } else {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          if (p0 + t < j.kw) w[t] = (uint32_t)s[t];
+          if (p0 + t < j.kw) w[t] = (uint32_t)src[t];
       }
-    } else {
+    };
+    row(r0, w0);
+    row(r1, w1);
+  } else {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        if (p0 + t < j.kw) w[t] = (uint32_t)j.src[(int64_t)(p0 + t) * j.ld + r];
+    for (int t = 0; t < 4; ++t) {
+      if (p0 + t >= j.kw) continue;
+      const int32_t* src = j.src + (int64_t)(p0 + t) * j.ld;
+      if (r0 < j.rows) w0[t] = (uint32_t)src[r0];
+      if (r1 < j.rows) w1[t] = (uint32_t)src[r1];
     }
   }
-  const uint64_t d0 = f6_codes8(w[0]), d1 = f6_codes8(w[1]), d2 = f6_codes8(w[2]), d3 = f6_codes8(w[3]);
-  const uint64_t u0 = d0 | (d1 << 48), u1 = (d1 >> 16) | (d2 << 32), u2 = (d2 >> 32) | (d3 << 16);
-  uint8_t* base = j.dst + ((int64_t)(r >> 5) * j.kblocks + kb) * kF6Pair + 16 * ((r & 15) + 16 * g);
+  const F6Lane x = f6_lane(w0), y = f6_lane(w1);
+  uint8_t* base = j.dst + ((int64_t)pr * j.kblocks + kb) * kF6Pair + 16 * (rr + 16 * g);
   typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
-  if (((r >> 4) & 1) == 0) {   // bits 0 .. 191: piece 0, low half of piece 1
-    *reinterpret_cast<u64x2*>(base) = u64x2{u0, u1};
-    *reinterpret_cast<uint64_t*>(base + 1024) = u2;
-  } else {                     // bits 192 .. 383: high half of piece 1, piece 2
-    *reinterpret_cast<uint64_t*>(base + 1024 + 8) = u0;
-    *reinterpret_cast<u64x2*>(base + 2048) = u64x2{u1, u2};
-  }
+  *reinterpret_cast<u64x2*>(base) = u64x2{x.u0, x.u1};          // bits 0 .. 127
+  *reinterpret_cast<u64x2*>(base + 1024) = u64x2{x.u2, y.u0};   // bits 128 .. 255
+  *reinterpret_cast<u64x2*>(base + 2048) = u64x2{y.u1, y.u2};   // bits 256 .. 383
 }
 
 // ---------------------------------------------------------------------------
@@ -397,8 +417,9 @@ F6Job f6_job(const int32_t* src, int64_t s_r, int64_t s_p, int64_t R, int64_t K,
   j.row_major = s_p == 1 ? 1 : 0;
   j.ld = j.row_major ? s_r : s_p;
   j.vec = j.row_major && (uintptr_t)src % 16 == 0 && s_r % 4 == 0;
-  // row-major: every 16-row group of every pair; columns: every 64 rows
-  j.blocks = j.row_major ? (int)((R + 31) / 32 * 2) * ((j.kblocks + 3) / 4) : (int)((R + 63) / 64) * j.kblocks;
+  // row-major: every pair x groups of 4 k-blocks; columns: groups of 4 pairs x every k-block
+  const int64_t pairs = (R + 31) / 32;
+  j.blocks = j.row_major ? (int)(pairs * ((j.kblocks + 3) / 4)) : (int)((pairs + 3) / 4 * j.kblocks);
   return j;
 }
 
