@@ -141,7 +141,9 @@ __device__ inline uint32_t out_bits(typename OT::T v) {
 // to C in 16-byte pieces, consecutive threads taking consecutive pieces of a
 // row (rows and columns past the matrix edge are skipped; C rows that are not
 // 16-byte aligned take element stores).
-template <int BM, int BN, int THREADS, class OT>
+// NT: the 16-byte pieces as non-temporal stores (streamed to memory instead of
+// kept dirty in L2).
+template <int BM, int BN, int THREADS, class OT, bool NT = false>
 __device__ __attribute__((always_inline)) inline void copy_out_c(const unsigned char* c_tile, int pitch, typename OT::T* out, int64_t ldc, int M,
                                   int N, int m0, int n0, int tid) {
   using T = typename OT::T;
@@ -157,7 +159,8 @@ __device__ __attribute__((always_inline)) inline void copy_out_c(const unsigned 
     const v4i d = *reinterpret_cast<const v4i*>(c_tile + row * pitch + 16 * q);
     T* o = out + (int64_t)m * ldc + n;
     if (vec && n + 7 < N) {
-      *reinterpret_cast<v4i*>(o) = d;
+      if constexpr (NT) __builtin_nontemporal_store(d, reinterpret_cast<v4i*>(o));
+      else *reinterpret_cast<v4i*>(o) = d;
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e)

@@ -401,7 +401,8 @@ gemm_f6_pp2(const uint8_t* __restrict__ a6, const uint8_t* __restrict__ b6, int 
     }
   }
   lds_barrier();
-  copy_out_c<BM / 2, BN, 256, OT>(c_half, C_PITCH, out, ldc, M, N, m0 + (grp1 ? BM / 2 : 0), n0, tid & 255);
+  // non-temporal: measured 140.6 -> 134.5 us at config 4 (no change at config 5's 256 tiles)
+  copy_out_c<BM / 2, BN, 256, OT, true>(c_half, C_PITCH, out, ldc, M, N, m0 + (grp1 ? BM / 2 : 0), n0, tid & 255);
   if (!grp1) bar();
 }
 
