@@ -300,6 +300,19 @@ def bench_linear(torch, tokens, steps, warmup, dev):
         f6 = {"convert_us": ms_c / steps * 1e3, "f6_gemm_kernel_us": ms_r / steps * 1e3}
     ms_s, wall = _time_graph(torch, lambda i: step(i % nbuf), steps, warmup)
     t_q, t_g, t_s = (ms / 1e3 / steps for ms in (ms_q, ms_g, ms_s))
+    if work is not None:
+        # the serving form of the same step: the weight converted to the FP6
+        # layout once (outside the timed region), only the codes per call
+        w6s = [capi.f6_convert(ws[j], LIN_K) for j in range(nbuf)]
+        a_ws = torch.empty(capi.f6_operand_bytes(tokens, LIN_K), dtype=torch.uint8, device=dev)
+
+        def step_f6w(j):
+            capi.w4a4_linear_f6w(xs[j], L, R, w6s[j], LIN_N, sw, 0.9, out=outs[j], codes=codes[j], scales=scales[j],
+                                 a_workspace=a_ws)
+
+        ms_p, _ = _time_graph(torch, lambda i: step_f6w(i % nbuf), steps, warmup)
+        f6["prepared_weight_us_per_step"] = ms_p / steps * 1e3
+        del w6s, a_ws
     ops = 2 * tokens * LIN_N * LIN_K
     gemm_gbs = g_bytes / t_g / 1e9
     out = {
@@ -699,6 +712,9 @@ BENCH_SEGMENTS = [
     ("cfg5 T=4096 f6 gemm alone", None, 2 * 4096 * LIN_N * LIN_K),
     ("cfg5 T=4096 step quant", _lin_q_bytes(4096), None), ("cfg5 T=4096 step convert", F6_CONVERT_BYTES_CFG5, None),
     ("cfg5 T=4096 step f6 gemm", None, 2 * 4096 * LIN_N * LIN_K),
+    ("cfg5 T=4096 f6w step quant", _lin_q_bytes(4096), None),
+    ("cfg5 T=4096 f6w step convert A", 4096 * LIN_K * 5 // 4, None),
+    ("cfg5 T=4096 f6w step f6 gemm", None, 2 * 4096 * LIN_N * LIN_K),
     ("quantize cfg1", 128 * 4096 * 4 + 128 * 4096 + 128 * 4 + 2 * 64 * 64 * 4, None),
     ("pack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
     ("unpack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
@@ -1121,7 +1137,9 @@ def main():
             lines[key] = bench_linear(torch, t, steps, warmup, dev)
             lines[key]["roofline"]["traffic"] = _traffic_from_profiles(f"gemm_cfg5_T{t}")
             _log(f"config 5 T={t}: {lines[key]['us_per_step']:.1f} us/step (quantize {lines[key]['quantize_us']:.1f}, "
-                 f"GEMM {lines[key]['gemm_us']:.1f})")
+                 f"GEMM {lines[key]['gemm_us']:.1f})"
+                 + (f"; weight converted once: {lines[key]['prepared_weight_us_per_step']:.1f} us/step"
+                    if "prepared_weight_us_per_step" in lines[key] else ""))
         _log("config 1 round trip + quantize")
         rt = roundtrip_cfg1(torch, dev)
         lines["quantize_cfg1"] = bench_quant(torch, wl.quant_cfg1(), steps, warmup, dev)

@@ -205,6 +205,23 @@ int64_t qo_int4_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int out_dty
  * QO_ERR_NULL_POINTER; QO_ERR_DTYPE (run: other out_dtype codes).
  */
 int64_t qo_int4_gemm_f6_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
+ * The FP6 route with each operand in a buffer of its own, for a weight
+ * converted once: qo_int4_gemm_f6_convert writes one operand of `rows` rows
+ * (A's rows, or B's columns: word p of row r at src[r * row_stride +
+ * p * word_stride], one stride 1) into dst (256-byte aligned,
+ * qo_int4_gemm_f6_operand_bytes(rows, K) bytes); qo_int4_gemm_f6_run2
+ * multiplies A (M rows) and B (N rows) held that way, with the arguments
+ * and results of qo_int4_gemm_f6_run. No counterpart in the reference.
+ */
+int64_t qo_int4_gemm_f6_operand_bytes(int64_t rows, int64_t K);
+int qo_int4_gemm_f6_convert(const int32_t* src, int64_t row_stride, int64_t word_stride, int64_t rows,
+                            int64_t K, void* dst, int64_t dst_bytes, void* stream);
+int qo_int4_gemm_f6_run2(const void* a6, int64_t a6_bytes, const void* b6, int64_t b6_bytes,
+                         const void* scale_a, int scale_a_dtype, const void* scale_b, int scale_b_dtype,
+                         const void* bias, void* out, int out_dtype, int64_t ldc,
+                         int64_t M, int64_t N, int64_t K, void* stream);
 int qo_int4_gemm_f6_prepare(const int32_t* a, int64_t lda,
                             const int32_t* b, int64_t b_stride_p, int64_t b_stride_n,
                             int64_t M, int64_t N, int64_t K,
@@ -259,6 +276,25 @@ int qo_w4a4_linear(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
  *
  * Errors: those of qo_w4a4_linear.
  */
+/*
+ * qo_w4a4_linear against a weight already converted to the FP6 operand layout
+ * (qo_int4_gemm_f6_convert(weight, weight_ld, 1, out_features, M*N, ...),
+ * once, weight_f6_bytes long): the codes of each call are converted into
+ * a_workspace (qo_int4_gemm_f6_operand_bytes(tokens, M*N) bytes) and
+ * multiplied on the FP6 route. Same outputs, codes and scales as
+ * qo_w4a4_linear bit for bit; x_dtype F16 or BF16, M*N <= 65536. For the
+ * serving step of a static weight (the per-call weight conversion of
+ * qo_w4a4_linear_ws is skipped); no counterpart in the reference.
+ *
+ * Errors: those of qo_w4a4_linear and qo_int4_gemm_f6_run2.
+ */
+int qo_w4a4_linear_f6w(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
+                       const void* left, const void* right, int M, int N, float clip_ratio,
+                       const void* weight_f6, int64_t weight_f6_bytes, int64_t out_features,
+                       const void* weight_scale, int weight_scale_dtype, const void* bias,
+                       int32_t* codes, float* act_scales, void* out, int64_t out_ld,
+                       void* a_workspace, int64_t a_workspace_bytes, void* stream);
+
 int qo_w4a4_linear_ws(const void* x, int x_dtype, int64_t tokens, int64_t x_ld,
                       const void* left, const void* right, int M, int N, float clip_ratio,
                       const int32_t* weight, int64_t weight_ld, int64_t out_features,

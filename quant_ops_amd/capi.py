@@ -21,7 +21,8 @@ STATUS = {0: "QO_OK", 1: "QO_ERR_NULL_POINTER", 2: "QO_ERR_SHAPE", 3: "QO_ERR_DT
 # Every symbol the header declares; the CPU tests check they are all exported.
 EXPORTED = ("qo_status_string", "qo_version", "qo_last_error", "qo_set_kernel_routing", "qo_flatquant_quantize",
             "qo_int4_gemm", "qo_int4_gemm_bias", "qo_int4_gemm_ws", "qo_int4_gemm_workspace_size", "qo_int4_gemm_f6_workspace_bytes",
-            "qo_int4_gemm_f6_prepare", "qo_int4_gemm_f6_run", "qo_w4a4_linear", "qo_w4a4_linear_ws", "qo_w4a4_linear_noalloc", "qo_dequantize_int4",
+            "qo_int4_gemm_f6_prepare", "qo_int4_gemm_f6_run", "qo_int4_gemm_f6_operand_bytes",
+            "qo_int4_gemm_f6_convert", "qo_int4_gemm_f6_run2", "qo_w4a4_linear_f6w", "qo_w4a4_linear", "qo_w4a4_linear_ws", "qo_w4a4_linear_noalloc", "qo_dequantize_int4",
             "qo_pack_int4_to_int32", "qo_unpack_int32_to_int4", "qo_transpose_int32")
 
 # QO_ROUTE_* bits of qo_set_kernel_routing (include/quant_ops_hip.h)
@@ -85,6 +86,16 @@ def lib():
     L.qo_w4a4_linear_ws.restype = c_int
     L.qo_w4a4_linear_ws.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_vp, c_i64, c_i64,
                                     c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp]
+    L.qo_int4_gemm_f6_operand_bytes.restype = c_i64
+    L.qo_int4_gemm_f6_operand_bytes.argtypes = [c_i64, c_i64]
+    L.qo_int4_gemm_f6_convert.restype = c_int
+    L.qo_int4_gemm_f6_convert.argtypes = [c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp]
+    L.qo_int4_gemm_f6_run2.restype = c_int
+    L.qo_int4_gemm_f6_run2.argtypes = [c_vp, c_i64, c_vp, c_i64, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_i64,
+                                       c_i64, c_i64, c_i64, c_vp]
+    L.qo_w4a4_linear_f6w.restype = c_int
+    L.qo_w4a4_linear_f6w.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_vp, c_i64, c_i64,
+                                     c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp]
     L.qo_w4a4_linear_noalloc.restype = c_int
     L.qo_w4a4_linear_noalloc.argtypes = [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_int, c_int, c_f, c_vp, c_i64,
                                          c_i64, c_vp, c_int, c_vp, c_vp, c_i64, c_vp]
@@ -237,6 +248,59 @@ def f6_run(workspace, m, n, k, scale_a, scale_b, out_dtype=torch.float16, out=No
         ctypes.c_void_p(out.data_ptr()), _TORCH_CODE[out.dtype], out.stride(0), m, n, k,
         ctypes.c_void_p(workspace.data_ptr()), workspace.numel(), _stream(stream)))
     return out
+
+
+def f6_operand_bytes(rows, k):
+    """``qo_int4_gemm_f6_operand_bytes``."""
+    return int(lib().qo_int4_gemm_f6_operand_bytes(rows, k))
+
+
+def f6_convert(src, k, rows_are_columns=False, out=None, stream=None):
+    """``qo_int4_gemm_f6_convert``: an operand in the FP6 layout. ``src`` int32
+    [rows, K/8] (A, or a [N, K/8] weight whose W.t() is B), or with
+    ``rows_are_columns`` a row-major [K/8, N] B. Returns the uint8 tensor."""
+    if rows_are_columns:
+        rows, rs, ws_ = src.shape[1], src.stride(1), src.stride(0)
+    else:
+        rows, rs, ws_ = src.shape[0], src.stride(0), src.stride(1)
+    n = f6_operand_bytes(rows, k)
+    if out is None:
+        out = torch.empty(n, dtype=torch.uint8, device=src.device)
+    _check(lib().qo_int4_gemm_f6_convert(ctypes.c_void_p(src.data_ptr()), rs, ws_, rows, k,
+                                         ctypes.c_void_p(out.data_ptr()), out.numel(), _stream(stream)))
+    return out
+
+
+def w4a4_linear_f6w(x, left, right, weight_f6, out_features, weight_scale, clip_ratio=1.0, bias=None, out=None,
+                    codes=None, scales=None, a_workspace=None, stream=None):
+    """``qo_w4a4_linear_f6w`` against ``weight_f6`` (``f6_convert(weight, M*N)`` of
+    the packed [out, M*N/8] weight). Returns (out, codes, scales)."""
+    t, f = x.shape
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    left, right = left.contiguous(), right.contiguous()
+    weight_scale = weight_scale.reshape(-1).contiguous()
+    m, n = left.shape[0], right.shape[0]
+    if codes is None:
+        codes = torch.empty((t, f // 8), dtype=torch.int32, device=x.device)
+    if scales is None:
+        scales = torch.empty((t,), dtype=torch.float32, device=x.device)
+    if out is None:
+        out = torch.empty((t, out_features), dtype=x.dtype, device=x.device)
+    if a_workspace is None:
+        a_workspace = torch.empty(max(1, f6_operand_bytes(t, f)), dtype=torch.uint8, device=x.device)
+    if bias is not None:
+        bias = bias.to(x.dtype).contiguous()
+    _check(lib().qo_w4a4_linear_f6w(
+        ctypes.c_void_p(x.data_ptr()), _TORCH_CODE[x.dtype], t, x.stride(0) if t else f,
+        ctypes.c_void_p(left.data_ptr()), ctypes.c_void_p(right.data_ptr()), m, n, float(clip_ratio),
+        ctypes.c_void_p(weight_f6.data_ptr()), weight_f6.numel(), out_features,
+        ctypes.c_void_p(weight_scale.data_ptr()), _TORCH_CODE[weight_scale.dtype],
+        ctypes.c_void_p(bias.data_ptr() if bias is not None else None),
+        ctypes.c_void_p(codes.data_ptr()), ctypes.c_void_p(scales.data_ptr()),
+        ctypes.c_void_p(out.data_ptr()), out.stride(0) if t else out_features,
+        ctypes.c_void_p(a_workspace.data_ptr()), a_workspace.numel(), _stream(stream)))
+    return out, codes, scales
 
 
 def w4a4_linear(x, left, right, weight, weight_scale, clip_ratio=1.0, bias=None, out=None, codes=None,

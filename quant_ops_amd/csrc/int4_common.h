@@ -186,5 +186,14 @@ void f6_prepare(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, in
 template <class OT>
 void f6_run(const void* sa, int sad, const void* sb, int sbd, typename OT::T* out, int64_t ldc,
             const typename OT::T* bias, int64_t M, int64_t N, int64_t K, const void* workspace, hipStream_t stream);
+// One operand (rows R: word p of row r at src[r * s_r + p * s_p], s_p or s_r
+// 1) converted into dst (f6_operand_bytes(R, K) bytes), and the GEMM on two
+// separately held operands (a prepared weight, converted once).
+int64_t f6_operand_bytes(int64_t rows, int64_t K);
+void f6_convert_operand(const int32_t* src, int64_t s_r, int64_t s_p, int64_t R, int64_t K, void* dst,
+                        hipStream_t stream);
+template <class OT>
+void f6_run2(const void* a6, const void* b6, const void* sa, int sad, const void* sb, int sbd, typename OT::T* out,
+             int64_t ldc, const typename OT::T* bias, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 }  // namespace qo

@@ -1598,3 +1598,69 @@ extern "C" int64_t qo_int4_gemm_f6_workspace_bytes(int64_t M, int64_t N, int64_t
   if (M < 1 || N < 1 || K < 8 || K > 65536) return 0;
   return qo::f6_workspace_bytes(M, N, K);
 }
+
+extern "C" int64_t qo_int4_gemm_f6_operand_bytes(int64_t rows, int64_t K) {
+  if (rows < 1 || K < 8 || K > 65536) return 0;
+  return qo::f6_operand_bytes(rows, K);
+}
+
+extern "C" int qo_int4_gemm_f6_convert(const int32_t* src, int64_t row_stride, int64_t word_stride, int64_t rows,
+                                       int64_t K, void* dst, int64_t dst_bytes, void* stream) {
+  const char* who = "qo_int4_gemm_f6_convert";
+  if (rows < 1 || K < 8 || K % 8 != 0 || K > 65536 || rows > INT32_MAX / 2) {
+    qo_set_error("%s: sizes rows=%lld K=%lld outside the FP6 route (K a multiple of 8 in 8 .. 65536)", who,
+                 (long long)rows, (long long)K);
+    return QO_ERR_SHAPE;
+  }
+  if (!src || !dst) {
+    qo_set_error("%s: NULL pointer argument", who);
+    return QO_ERR_NULL_POINTER;
+  }
+  if ((word_stride != 1 && row_stride != 1) || (word_stride == 1 && rows > 1 && row_stride < K / 8) ||
+      (row_stride == 1 && word_stride != 1 && word_stride < rows) || (uintptr_t)dst % 256 != 0 ||
+      dst_bytes < qo::f6_operand_bytes(rows, K)) {
+    qo_set_error("%s: strides (%lld, %lld) need a unit stride and no overlap; dst 256-byte aligned, %lld bytes", who,
+                 (long long)row_stride, (long long)word_stride, (long long)qo::f6_operand_bytes(rows, K));
+    return QO_ERR_SHAPE;
+  }
+  qo::launch_begin();
+  qo::f6_convert_operand(src, row_stride, word_stride, rows, K, dst, reinterpret_cast<hipStream_t>(stream));
+  return qo::launch_result(who);
+}
+
+extern "C" int qo_int4_gemm_f6_run2(const void* a6, int64_t a6_bytes, const void* b6, int64_t b6_bytes,
+                                    const void* scale_a, int scale_a_dtype, const void* scale_b, int scale_b_dtype,
+                                    const void* bias, void* out, int out_dtype, int64_t ldc, int64_t M, int64_t N,
+                                    int64_t K, void* stream) {
+  using namespace qo;
+  const char* who = "qo_int4_gemm_f6_run2";
+  if (M < 1 || N < 1 || K < 8 || K % 8 != 0 || K > 65536 || M > INT32_MAX / 2 || N > INT32_MAX / 2) {
+    qo_set_error("%s: sizes M=%lld N=%lld K=%lld outside the FP6 route", who, (long long)M, (long long)N,
+                 (long long)K);
+    return QO_ERR_SHAPE;
+  }
+  if (!a6 || !b6 || !scale_a || !scale_b || !out) {
+    qo_set_error("%s: NULL pointer argument", who);
+    return QO_ERR_NULL_POINTER;
+  }
+  if (a6_bytes < f6_operand_bytes(M, K) || b6_bytes < f6_operand_bytes(N, K) || ldc < N) {
+    qo_set_error("%s: operand buffers below %lld / %lld bytes or ldc below N", who,
+                 (long long)f6_operand_bytes(M, K), (long long)f6_operand_bytes(N, K));
+    return QO_ERR_SHAPE;
+  }
+  if (!is_float_code(scale_a_dtype) || !is_float_code(scale_b_dtype) ||
+      (out_dtype != QO_DTYPE_F16 && out_dtype != QO_DTYPE_BF16)) {
+    qo_set_error("%s: unsupported dtype codes (scale_a=%d, scale_b=%d, out=%d; out must be F16 or BF16)", who,
+                 scale_a_dtype, scale_b_dtype, out_dtype);
+    return QO_ERR_DTYPE;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  launch_begin();
+  if (out_dtype == QO_DTYPE_F16)
+    f6_run2<OutF16>(a6, b6, scale_a, scale_a_dtype, scale_b, scale_b_dtype, static_cast<_Float16*>(out), ldc,
+                    static_cast<const _Float16*>(bias), M, N, K, s);
+  else
+    f6_run2<OutBF16>(a6, b6, scale_a, scale_a_dtype, scale_b, scale_b_dtype, static_cast<__bf16*>(out), ldc,
+                     static_cast<const __bf16*>(bias), M, N, K, s);
+  return launch_result(who);
+}

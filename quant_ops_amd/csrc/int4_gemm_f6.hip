@@ -455,12 +455,25 @@ void f6_prepare(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp, in
   if (ja.blocks + jb.blocks > 0) launch(f6_convert_kernel, dim3(ja.blocks + jb.blocks), dim3(256), 0, stream, ja, jb);
 }
 
+void f6_convert_operand(const int32_t* src, int64_t s_r, int64_t s_p, int64_t R, int64_t K, void* dst,
+                        hipStream_t stream) {
+  const F6Job j = f6_job(src, s_r, s_p, R, K, static_cast<uint8_t*>(dst));
+  if (j.blocks > 0) launch(f6_convert_kernel, dim3(j.blocks), dim3(256), 0, stream, j, F6Job{});
+}
+
 template <class OT>
 void f6_run(const void* sa, int sad, const void* sb, int sbd, typename OT::T* out, int64_t ldc,
             const typename OT::T* bias, int64_t M, int64_t N, int64_t K, const void* workspace, hipStream_t stream) {
-  constexpr int BM = 256;
   const uint8_t* a6 = static_cast<const uint8_t*>(workspace);
-  const uint8_t* b6 = a6 + align256(f6_operand_bytes(M, K));
+  f6_run2<OT>(a6, a6 + align256(f6_operand_bytes(M, K)), sa, sad, sb, sbd, out, ldc, bias, M, N, K, stream);
+}
+
+template <class OT>
+void f6_run2(const void* a6v, const void* b6v, const void* sa, int sad, const void* sb, int sbd, typename OT::T* out,
+             int64_t ldc, const typename OT::T* bias, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  constexpr int BM = 256;
+  const uint8_t* a6 = static_cast<const uint8_t*>(a6v);
+  const uint8_t* b6 = static_cast<const uint8_t*>(b6v);
   const bool wide = f6_wide(M, N);
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + (wide ? 255 : 223)) / (wide ? 256 : 224));
   auto go = [&](auto kernel) {
@@ -479,6 +492,10 @@ void f6_gemm_launch(const int32_t* a, int64_t lda, const int32_t* b, int64_t bsp
   f6_run<OT>(sa, sad, sb, sbd, out, ldc, bias, M, N, K, workspace, stream);
 }
 
+template void f6_run2<OutF16>(const void*, const void*, const void*, int, const void*, int, _Float16*, int64_t,
+                              const _Float16*, int64_t, int64_t, int64_t, hipStream_t);
+template void f6_run2<OutBF16>(const void*, const void*, const void*, int, const void*, int, __bf16*, int64_t,
+                               const __bf16*, int64_t, int64_t, int64_t, hipStream_t);
 template void f6_run<OutF16>(const void*, int, const void*, int, _Float16*, int64_t, const _Float16*, int64_t, int64_t,
                              int64_t, const void*, hipStream_t);
 template void f6_run<OutBF16>(const void*, int, const void*, int, __bf16*, int64_t, const __bf16*, int64_t, int64_t,

@@ -106,6 +106,45 @@ extern "C" int qo_w4a4_linear_ws(const void* x, int x_dtype, int64_t tokens, int
                     workspace, workspace_bytes);
 }
 
+// The linear layer against a weight already in the FP6 operand layout
+// (qo_int4_gemm_f6_convert of its [out, in/8] rows, done once): quantize, the
+// codes converted into a_workspace, then the FP6 GEMM.
+extern "C" int qo_w4a4_linear_f6w(const void* x, int x_dtype, int64_t tokens, int64_t x_ld, const void* left,
+                                  const void* right, int M, int N, float clip_ratio, const void* weight_f6,
+                                  int64_t weight_f6_bytes, int64_t out_features, const void* weight_scale,
+                                  int weight_scale_dtype, const void* bias, int32_t* codes, float* act_scales,
+                                  void* out, int64_t out_ld, void* a_workspace, int64_t a_workspace_bytes,
+                                  void* stream) {
+  using namespace qo;
+  const char* fn = "qo_w4a4_linear_f6w";
+  const int64_t features = (int64_t)M * N;
+  if (tokens < 0 || M < 1 || N < 1 || out_features < 1 || features % 8 != 0 || x_ld < features ||
+      out_ld < out_features || features > 65536) {
+    qo_set_error("%s: invalid sizes or strides (tokens=%lld M=%d N=%d out_features=%lld)", fn, (long long)tokens, M, N,
+                 (long long)out_features);
+    return QO_ERR_SHAPE;
+  }
+  if (x_dtype != QO_DTYPE_F16 && x_dtype != QO_DTYPE_BF16) {
+    qo_set_error("%s: input dtype code %d (the FP6 GEMM writes 16-bit outputs: F16 or BF16)", fn, x_dtype);
+    return QO_ERR_DTYPE;
+  }
+  if (tokens == 0) return QO_OK;
+  if (!weight_f6 || !a_workspace || !codes || !act_scales) {
+    qo_set_error("%s: NULL pointer argument", fn);
+    return QO_ERR_NULL_POINTER;
+  }
+  const int q = flatquant_quantize(x, x_dtype, tokens, x_ld, left, right, M, N, clip_ratio, 1, codes, act_scales,
+                                   stream, ReadAhead{});
+  if (q != QO_OK) return inner_failed(fn, q);
+  const int c = qo_int4_gemm_f6_convert(codes, features / 8, 1, tokens, features, a_workspace, a_workspace_bytes,
+                                        stream);
+  if (c != QO_OK) return inner_failed(fn, c);
+  const int g = qo_int4_gemm_f6_run2(a_workspace, a_workspace_bytes, weight_f6, weight_f6_bytes, act_scales,
+                                     QO_DTYPE_F32, weight_scale, weight_scale_dtype, bias, out, x_dtype, out_ld, tokens,
+                                     out_features, features, stream);
+  return g == QO_OK ? g : inner_failed(fn, g);
+}
+
 // ---------------------------------------------------------------------------
 // The linear layer without caller buffers for the activation codes and
 // scales: they are staged in `scratch`, one array per GPU that lives as long

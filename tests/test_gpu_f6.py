@@ -226,3 +226,51 @@ def test_linear_torch_operator_large_tokens(gpu):
     y, _, _ = capi.w4a4_linear(*args, 0.9, bias.to(gpu))
     torch.cuda.synchronize()
     assert torch.equal(y_op, y)
+
+
+@pytest.mark.parametrize("tokens,m,n,out_f,dtype", [(300, 112, 128, 272, torch.bfloat16), (1024, 64, 128, 1000,
+                                                   torch.float16), (40, 112, 128, 512, torch.bfloat16)])
+def test_linear_prepared_f6_weight(gpu, tokens, m, n, out_f, dtype):
+    """qo_w4a4_linear_f6w against a weight converted once (qo_int4_gemm_f6_convert)
+    equals qo_w4a4_linear bit for bit (outputs, codes, scales); the same
+    converted weight serves two calls."""
+    from test_gpu_parity import _linear_inputs
+
+    _say(f"linear f6w T={tokens} {m}x{n} -> {out_f} {dtype}")
+    x, L, R, w, sw, bias = _linear_inputs(tokens, m, n, out_f, dtype, 1200 + tokens)
+    Ld, Rd, wd, swd, bd = L.to(gpu), R.to(gpu), w.to(gpu), sw.to(gpu), bias.to(gpu)
+    w6 = capi.f6_convert(wd, m * n)
+    for rep in range(2):
+        xd = x.to(gpu) if rep == 0 else (x * 0.5).to(dtype).to(gpu)
+        y6, q6, s6 = capi.w4a4_linear_f6w(xd, Ld, Rd, w6, out_f, swd, 0.9, bd)
+        y, q, s = capi.w4a4_linear(xd, Ld, Rd, wd, swd, 0.9, bd)
+        torch.cuda.synchronize()
+        assert torch.equal(q6, q) and torch.equal(s6, s), f"call {rep}"
+        assert torch.equal(y6, y), f"call {rep}"
+
+
+def test_operand_convert_and_run2_match_workspace_route(gpu):
+    """qo_int4_gemm_f6_convert of A and of a row-major [K/8, N] B, then
+    qo_int4_gemm_f6_run2, equals qo_int4_gemm_ws; the error paths reject
+    short buffers."""
+    m, n, k = 640, 700, 1152
+    case = wl.gemm_case(m, n, k, seed=1300)
+    a, b, sa, sb = case.a.to(gpu), case.b.to(gpu), case.scale_a.to(gpu), case.scale_b.to(gpu)
+    a6 = capi.f6_convert(a, k)
+    b6 = capi.f6_convert(b, k, rows_are_columns=True)
+    out = torch.empty(m, n, dtype=torch.float16, device=gpu)
+    capi._check(capi.lib().qo_int4_gemm_f6_run2(
+        ctypes.c_void_p(a6.data_ptr()), a6.numel(), ctypes.c_void_p(b6.data_ptr()), b6.numel(),
+        ctypes.c_void_p(sa.data_ptr()), capi.DTYPE_F16, ctypes.c_void_p(sb.data_ptr()), capi.DTYPE_F16, None,
+        ctypes.c_void_p(out.data_ptr()), capi.DTYPE_F16, n, m, n, k,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    ref = capi.int4_gemm(a, b, sa, sb, workspace=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    st = capi.lib().qo_int4_gemm_f6_run2(
+        ctypes.c_void_p(a6.data_ptr()), a6.numel() - 1, ctypes.c_void_p(b6.data_ptr()), b6.numel(),
+        ctypes.c_void_p(sa.data_ptr()), capi.DTYPE_F16, ctypes.c_void_p(sb.data_ptr()), capi.DTYPE_F16, None,
+        ctypes.c_void_p(out.data_ptr()), capi.DTYPE_F16, n, m, n, k, None)
+    assert st != 0
+    with pytest.raises(capi.QuantOpsError):
+        capi.f6_convert(a, k, out=torch.empty(16, dtype=torch.uint8, device=gpu))
