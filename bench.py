@@ -712,8 +712,10 @@ BENCH_SEGMENTS = [
     ("cfg5 T=4096 f6 gemm alone", None, 2 * 4096 * LIN_N * LIN_K),
     ("cfg5 T=4096 step quant", _lin_q_bytes(4096), None), ("cfg5 T=4096 step convert", F6_CONVERT_BYTES_CFG5, None),
     ("cfg5 T=4096 step f6 gemm", None, 2 * 4096 * LIN_N * LIN_K),
-    ("cfg5 T=4096 f6w step quant", _lin_q_bytes(4096), None),
+    # (the weight's one-time conversion has the A conversion's grid, so their
+    # segment is dispatched first)
     ("cfg5 T=4096 f6w step convert A", 4096 * LIN_K * 5 // 4, None),
+    ("cfg5 T=4096 f6w step quant", _lin_q_bytes(4096), None),
     ("cfg5 T=4096 f6w step f6 gemm", None, 2 * 4096 * LIN_N * LIN_K),
     ("quantize cfg1", 128 * 4096 * 4 + 128 * 4096 + 128 * 4 + 2 * 64 * 64 * 4, None),
     ("pack cfg4 weight", 14336 * 4096 + 14336 * 512 * 4, None),
