@@ -7,7 +7,9 @@ clip ratios and both code layouts, with a few zero tokens; codes and scales
 checked with check_quant's tolerances. GEMM: random M, N, K (K a multiple of
 8), both B layouts, output dtypes and scale dtypes, with and without bias;
 every output bit-exact against int4_matmul_pytorch (int4_matmul/ops.py:69-103)
-plus the reference's bias addition. Each case prints its parameters first, so
+plus the reference's bias addition, on the integer kernels and (16-bit
+outputs) on the FP6 route, through the workspace entry point and through
+prepare / run at every M. Each case prints its parameters first, so
 a failure names its case.
 """
 import random
@@ -85,3 +87,15 @@ def test_gemm_random_case(gpu, i):
     if bias is not None:
         ref = ref + bias
     assert torch.equal(out.cpu(), ref)
+    if odt != torch.float32:
+        # the same call with a workspace (the FP6 route above 256 rows) and the
+        # FP6 kernels at any M through prepare / run
+        out_ws = capi.int4_gemm(case.a.to(gpu), case.b.to(gpu), sa.to(gpu), sb.to(gpu), out_dtype=odt,
+                                bias=None if bias is None else bias.to(gpu), workspace=True)
+        ws = torch.empty(capi.f6_workspace_bytes(m, n, k), dtype=torch.uint8, device=gpu)
+        capi.f6_prepare(ws, m, n, k, a=case.a.to(gpu), b=case.b.to(gpu))
+        out_f6 = capi.f6_run(ws, m, n, k, sa.to(gpu), sb.to(gpu), out_dtype=odt,
+                             bias=None if bias is None else bias.to(gpu))
+        torch.cuda.synchronize()
+        assert torch.equal(out_ws.cpu(), ref)
+        assert torch.equal(out_f6.cpu(), ref)
