@@ -914,6 +914,19 @@ def ceilings(torch, steps, warmup, dev):
                  f"{ops / (us * 1e-6) / 1e12:.0f} TOP/s")
     out["mfma_f6_operands_from_memory"] = f6
 
+    # FP6 MFMAs on one wave per SIMD and 16-byte LDS reads on the other, apart and together
+    lib.qo_probe_mfma_lds_overlap.argtypes = [c_int, c_int, c_int, c_vp, c_vp]
+    ovl = {}
+    for mode, name in ((1, "mfma_only"), (2, "lds_reads_only"), (3, "both")):
+        def launch(i, mode=mode):
+            assert lib.qo_probe_mfma_lds_overlap(mode, cus, iters, ctypes.c_void_p(fsink.data_ptr()), stream()) == 0
+        ms, _ = _time_graph(torch, launch, steps, warmup)
+        ovl[name] = ms / steps * 1e3
+    ovl["both_over_longer"] = ovl["both"] / max(ovl["mfma_only"], ovl["lds_reads_only"])
+    _log(f"ceiling: FP6 MFMA wave + LDS-read wave per SIMD: {ovl['mfma_only']:.0f} / {ovl['lds_reads_only']:.0f} us "
+         f"apart, {ovl['both']:.0f} us together ({ovl['both_over_longer']:.2f} x the longer)")
+    out["mfma_lds_overlap_us"] = ovl
+
     def launch_empty(i):
         assert lib.qo_probe_empty(stream()) == 0
     ms, _ = _time_graph(torch, launch_empty, steps, warmup)

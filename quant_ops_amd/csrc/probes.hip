@@ -13,6 +13,9 @@
 //    (v_mfma_scale_f32_16x16x128_f8f6f4, both operands FP6 e2m3, block
 //    scales 2^3 as the FP6 GEMM route uses them), 32-byte operands of which
 //    the instruction reads 24;
+//  * qo_probe_mfma_lds_overlap: one wave per SIMD issuing FP6 MFMAs, the
+//    other issuing 16-byte LDS reads (either alone, or both), to see how far
+//    the two overlap on one SIMD (the FP6 GEMM's ping-pong relies on it);
 //  * qo_probe_empty: an empty kernel (launch and wave start-up cost);
 //  * qo_probe_stream: a streaming kernel with the quantize's traffic shape,
 //    16 bytes read and 4 bytes written per lane per step (config 2 reads
@@ -134,6 +137,37 @@ __global__ void __launch_bounds__(512) probe_mfma_f6_data(int iters, const v8i* 
   if (lane == 0) cycles[blockIdx.x * (blockDim.x >> 6) + wave] = t1 - t0;
 }
 
+// 512 threads: waves 0-3 (one per SIMD) run FP6 MFMAs when mode bit 0 is set,
+// waves 4-7 run ds_read_b128 loops (4 x 1 KiB per iteration) when bit 1 is.
+__global__ void __launch_bounds__(512) probe_mfma_lds_overlap(int mode, int iters, float* out) {
+  __shared__ __align__(16) unsigned char buf[65536];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  for (int i = t; i < 16384; i += 512) reinterpret_cast<int*>(buf)[i] = i;
+  __syncthreads();
+  float s = 0.f;
+  if (wave < 4) {
+    if (mode & 1) {
+      const v8i a = {t, 1, 2, 3, 4, 5, 6, 7}, b = {7, 6, 5, 4, 3, 2, 1, t};
+      v4f acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int it = 0; it < iters; ++it)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[j], 2, 2, 0, 127, 0, 127);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += acc[j][0];
+    }
+  } else if (mode & 2) {
+    v4i acc = {0, 0, 0, 0};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc ^= *reinterpret_cast<const v4i*>(buf + ((wave * 4 + k + it) & 31) * 2048 + 16 * lane);
+    s = (float)(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]);
+  }
+  out[blockIdx.x * 512 + t] = s;
+}
+
 __global__ void probe_empty() {}
 
 // grid-stride: 16 bytes in, their four words XORed into 4 bytes out
@@ -187,6 +221,13 @@ extern "C" int qo_probe_mfma_f6_data(int kvalu, int blocks, int iters, const voi
     case 2: probe_mfma_f6_data<2><<<blocks, 512, 0, s>>>(iters, v, out, cycles); break;
     default: return 1;
   }
+  return (int)hipGetLastError();
+}
+
+// mode 1: MFMAs only, 2: LDS reads only, 3: both; out: blocks x 512 floats
+extern "C" int qo_probe_mfma_lds_overlap(int mode, int blocks, int iters, float* out, void* stream) {
+  if (mode < 1 || mode > 3) return 1;
+  probe_mfma_lds_overlap<<<blocks, 512, 0, reinterpret_cast<hipStream_t>(stream)>>>(mode, iters, out);
   return (int)hipGetLastError();
 }
 
