@@ -511,55 +511,75 @@ struct FqEpi<BF16T> {
     return word;
   }
 
-  // The same word through byte packing: t = rnd(y * rcp) for the pair (one
-  // v_cvt_pk), the upper clamp on the packed pair as signed 16-bit integers
-  // (non-negative bf16 patterns order like their values, negative ones are
-  // negative integers, so min with 7.0's pattern clamps only t > 7), then
-  // v_cvt_pk_u8_f32 of t + 8 (exact) rounds half to even and saturates at 0,
-  // which is round-half-even of t and the lower clamp at -8, offset by 8.
-  // Even codes go to bytes of `ev`, odd codes to bytes of `od`; ev | od << 4
-  // puts code i in nibble i.
-  __device__ static inline uint32_t word_u8(const uint32_t (&p)[4], float rcp) {
-    typedef short v2s __attribute__((ext_vector_type(2)));
-    const v2s seven = {(short)0x40E0, (short)0x40E0};
-    uint32_t ev = 0u, od = 0u;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      // one v_cvt_pk_bf16_f32 for the pair (written out: as two conversions
-      // feeding a 16-bit integer min, the compiler emits two converts and a
-      // v_perm). Its operands are VALU products, never MFMA results.
-      uint32_t tp;
-      asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(tp) : "v"(lo(p[r]) * rcp), "v"(hi(p[r]) * rcp));
-      v2s t = __builtin_bit_cast(v2s, tp);
-      t = __builtin_elementwise_min(t, seven);
-      const uint32_t tb = __builtin_bit_cast(uint32_t, t);
-      const float f0 = lo(tb) + 8.0f, f1 = hi(tb) + 8.0f;   // codes r and r + 4
-      uint32_t& d = (r & 1) ? od : ev;
-      d = __builtin_amdgcn_cvt_pk_u8_f32(f0, r >> 1, d);
-      d = __builtin_amdgcn_cvt_pk_u8_f32(f1, 2 + (r >> 1), d);
-    }
+  // Code byte B of d from a rounded quotient t (a bf16 value in a float32
+  // register, -8.5 <= t < 7.5): one SDWA add of 12582920 = 1.5 * 2^23 + 8,
+  // whose float32 sum has a unit ulp, so it rounds t + 8 half to even, which
+  // is rint(t) + 8 (8 is even), and leaves that integer (0 .. 15) in the
+  // low byte of its bits; dst_sel writes that byte into byte B of d, the
+  // other bytes kept (FIRST: cleared). A NaN t (its float32 low half zero)
+  // gives byte 0, as v_cvt_pk_u8_f32 of t + 8 does.
+  template <int B, bool FIRST>
+  __device__ static inline void code_byte(uint32_t& d, float t, float magic) {
+    static_assert(!FIRST || B == 0, "the first byte of a word clears the rest");
+#define QO_CODE_BYTE(SEL, UNUSED, C)                                                                         \
+  asm("v_add_f32_sdwa %0, %1, %2 dst_sel:" SEL " dst_unused:" UNUSED " src0_sel:DWORD src1_sel:DWORD"     \
+      : C(d)                                                                                                \
+      : "v"(t), "v"(magic))
+    if constexpr (FIRST) QO_CODE_BYTE("BYTE_0", "UNUSED_PAD", "=v");
+    else if constexpr (B == 1) QO_CODE_BYTE("BYTE_1", "UNUSED_PRESERVE", "+v");
+    else if constexpr (B == 2) QO_CODE_BYTE("BYTE_2", "UNUSED_PRESERVE", "+v");
+    else QO_CODE_BYTE("BYTE_3", "UNUSED_PRESERVE", "+v");
+#undef QO_CODE_BYTE
+  }
+
+  // The packed word of four pairs from rounded quotients t[i] (code i):
+  // even codes in the bytes of ev, odd codes in the bytes of od, and
+  // ev | od << 4 puts code i in nibble i.
+  __device__ static inline uint32_t word_from_quotients(const float (&t)[8]) {
+    const float magic = 12582920.0f;
+    uint32_t ev, od;
+    code_byte<0, true>(ev, t[0], magic);
+    code_byte<0, true>(od, t[1], magic);
+    code_byte<1, false>(ev, t[2], magic);
+    code_byte<1, false>(od, t[3], magic);
+    code_byte<2, false>(ev, t[4], magic);
+    code_byte<2, false>(od, t[5], magic);
+    code_byte<3, false>(ev, t[6], magic);
+    code_byte<3, false>(od, t[7], magic);
     return ev | (od << 4);
   }
 
-  // word_u8 for a token whose largest quotient rounds below 7.5 (every code
-  // then lies in -8 .. 7 without the upper clamp; the lower one is the u8
-  // conversion's saturation at 0 either way): each quotient is rounded to
-  // bf16 straight into a float32 register by one v_cvt_pk_bf16_f32 whose low
-  // half is the conversion of 0.0 (the bf16 value's float32 bits, low half
-  // zero), so no unpacking of a rounded pair is needed: 10 VALU per pair of
-  // codes instead of 12.
-  __device__ static inline uint32_t word_u8_noclamp(const uint32_t (&p)[4], float rcp) {
-    uint32_t ev = 0u, od = 0u;
+  // The same word as word4 through code bytes: per code the quotient
+  // y * rcp clamped to [-8, 7] (v_med3; the clamp commutes with the rounding
+  // since -8 and 7 are bf16 values), rounded to bf16 straight into a float32
+  // register by one v_cvt_pk_bf16_f32 whose low half is the conversion of 0.0
+  // (the bf16 value's float32 bits, low half zero), then code_byte: 10 VALU
+  // per pair of codes (the two elements unpacked, two products, two clamps,
+  // two conversions, two code bytes).
+  __device__ static inline uint32_t word_u8(const uint32_t (&p)[4], float rcp) {
+    float t[8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float t0, t1;   // operands are VALU products, never MFMA results
-      asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(t0) : "v"(lo(p[r]) * rcp));
-      asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(t1) : "v"(hi(p[r]) * rcp));
-      uint32_t& d = (r & 1) ? od : ev;
-      d = __builtin_amdgcn_cvt_pk_u8_f32(t0 + 8.0f, r >> 1, d);
-      d = __builtin_amdgcn_cvt_pk_u8_f32(t1 + 8.0f, 2 + (r >> 1), d);
+      // operands are VALU results, never MFMA results
+      asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(t[r]) : "v"(__builtin_amdgcn_fmed3f(lo(p[r]) * rcp, -8.0f, 7.0f)));
+      asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(t[r + 4]) : "v"(__builtin_amdgcn_fmed3f(hi(p[r]) * rcp, -8.0f, 7.0f)));
     }
-    return ev | (od << 4);
+    return word_from_quotients(t);
+  }
+
+  // word_u8 for a token whose largest quotient rounds below 7.5 and whose
+  // smallest rounds to -8.5 or above (every code then lies in -8 .. 7 with
+  // no clamp; the host picks this form from the clip ratio, kNoClampClip):
+  // 8 VALU per pair of codes.
+  __device__ static inline uint32_t word_u8_noclamp(const uint32_t (&p)[4], float rcp) {
+    float t[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      // operands are VALU products, never MFMA results
+      asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(t[r]) : "v"(lo(p[r]) * rcp));
+      asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(t[r + 4]) : "v"(hi(p[r]) * rcp));
+    }
+    return word_from_quotients(t);
   }
 
   // max |y| of rounded Y pairs as a 16-bit pattern (sign-cleared bf16 bits
@@ -2460,7 +2480,8 @@ constexpr int64_t kFewTwoSlots = 2;
 // largest quotient u = fl(amax rcp) <= 7 (1 + 2^-24)^2 / (c (1 - 2^-24)^2
 // (1 - 2^-8)^2), which is below 7.484375 (the least float32 that rounds to
 // bf16 7.5 or above) for c > 0.9427. The clamp of the scale at rnd(1e-8)
-// only makes s larger.
+// only makes s larger. No lower clamp is needed either: |y| <= amax and both
+// roundings are sign-symmetric, so the smallest quotient is above -7.5.
 constexpr float kNoClampClip = 0.95f;
 
 template <class DT, int MB, bool PACK>
