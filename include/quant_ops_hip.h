@@ -212,8 +212,9 @@ int64_t qo_int4_gemm_f6_workspace_bytes(int64_t M, int64_t N, int64_t K);
  * (A's rows, or B's columns: word p of row r at src[r * row_stride +
  * p * word_stride], one stride 1) into dst (256-byte aligned,
  * qo_int4_gemm_f6_operand_bytes(rows, K) bytes); qo_int4_gemm_f6_run2
- * multiplies A (M rows) and B (N rows) held that way, with the arguments
- * and results of qo_int4_gemm_f6_run. No counterpart in the reference.
+ * multiplies A (M rows) and B (N rows) held that way (both buffers 256-byte
+ * aligned, QO_ERR_SHAPE otherwise), with the arguments and results of
+ * qo_int4_gemm_f6_run. No counterpart in the reference.
  */
 int64_t qo_int4_gemm_f6_operand_bytes(int64_t rows, int64_t K);
 int qo_int4_gemm_f6_convert(const int32_t* src, int64_t row_stride, int64_t word_stride, int64_t rows,

@@ -1648,6 +1648,10 @@ extern "C" int qo_int4_gemm_f6_run2(const void* a6, int64_t a6_bytes, const void
                  (long long)f6_operand_bytes(M, K), (long long)f6_operand_bytes(N, K));
     return QO_ERR_SHAPE;
   }
+  if ((uintptr_t)a6 % 256 != 0 || (uintptr_t)b6 % 256 != 0) {
+    qo_set_error("%s: operand buffers must be 256-byte aligned (as qo_int4_gemm_f6_convert writes them)", who);
+    return QO_ERR_SHAPE;
+  }
   if (!is_float_code(scale_a_dtype) || !is_float_code(scale_b_dtype) ||
       (out_dtype != QO_DTYPE_F16 && out_dtype != QO_DTYPE_BF16)) {
     qo_set_error("%s: unsupported dtype codes (scale_a=%d, scale_b=%d, out=%d; out must be F16 or BF16)", who,

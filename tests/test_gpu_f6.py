@@ -272,5 +272,11 @@ def test_operand_convert_and_run2_match_workspace_route(gpu):
         ctypes.c_void_p(sa.data_ptr()), capi.DTYPE_F16, ctypes.c_void_p(sb.data_ptr()), capi.DTYPE_F16, None,
         ctypes.c_void_p(out.data_ptr()), capi.DTYPE_F16, n, m, n, k, None)
     assert st != 0
+    b6_off = torch.empty(b6.numel() + 256, dtype=torch.uint8, device=gpu)[16:]   # 16 bytes past 256
+    st = capi.lib().qo_int4_gemm_f6_run2(
+        ctypes.c_void_p(a6.data_ptr()), a6.numel(), ctypes.c_void_p(b6_off.data_ptr()), b6.numel(),
+        ctypes.c_void_p(sa.data_ptr()), capi.DTYPE_F16, ctypes.c_void_p(sb.data_ptr()), capi.DTYPE_F16, None,
+        ctypes.c_void_p(out.data_ptr()), capi.DTYPE_F16, n, m, n, k, None)
+    assert st != 0 and "256-byte aligned" in capi.lib().qo_last_error().decode()
     with pytest.raises(capi.QuantOpsError):
         capi.f6_convert(a, k, out=torch.empty(16, dtype=torch.uint8, device=gpu))
