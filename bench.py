@@ -38,7 +38,7 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--warm-s 0.2] [--no
        python bench.py --pmc-pass                       (under rocprofv3 --pmc FETCH_SIZE or WRITE_SIZE)
        python bench.py --pmc-summary FETCH_DIR WRITE_DIR
        python bench.py --pmc-table PMC_DIR [PMC_DIR ...]
-       python bench.py --ceilings                       (int8 MFMA rate, empty launch, streaming copy)
+       python bench.py --ceilings                       (MFMA rates, LDS-DMA and LDS reads, empty launch, streaming copy)
        python bench.py --power                          (board power and clock while each kernel loops)
        python bench.py --ceilings-summary KERNEL_TRACE_CSV
        python bench.py --trace-summary KERNEL_TRACE_CSV [--trace-last K]
@@ -751,6 +751,8 @@ def ceilings_summary(trace_csv):
         elif short.startswith("probe_mfma_f6"):
             waves = grid // 64   # rows mix the zero, int4-code and random-field runs; bench.py's log splits them
             rate = f"{2 * 16 * 16 * 128 * 8 * 4096 * waves / (med * 1e-6) / 1e12:.0f} TOP/s (median)"
+        elif short.startswith("probe_lds_dma"):
+            rate = "modes 1-3 in call order: copies, reads, four waves each"
         elif short.startswith("probe_stream"):
             rate = f"{2048 * 4096 * 2 * 5 / 4 / (med * 1e-6) / 1e9:.0f} GB/s (median)"
         print(f"{short:28s} {block:5d} {grid:9d} {len(v):6d} {avg:9.2f} {med:9.2f}  {rate}")
@@ -840,9 +842,11 @@ def _f6_probe_operands(torch, g, int4):
 def ceilings(torch, steps, warmup, dev):
     """Microbenchmarks of the ceilings the kernels are compared with
     (libquant_ops_probes.so): the int8 MFMA rate with 0-8 independent VALU
-    instructions per MFMA (two waves per SIMD on every CU), an empty kernel's
-    launch in a graph, and a streaming kernel moving config 2's bytes (16.8 MB
-    in, 4.2 MB out). Each is timed like the workloads (graph of ``steps``
+    instructions per MFMA (two waves per SIMD on every CU), the same on
+    operands from memory and for the FP6 matrix cores, FP6 MFMAs beside LDS
+    reads, LDS-DMA copies from L2 beside LDS reads, an empty kernel's launch
+    in a graph, and a streaming kernel moving config 2's bytes (16.8 MB in,
+    4.2 MB out). Each is timed like the workloads (graph of ``steps``
     launches, HIP events); one JSON line."""
     import ctypes
 
@@ -926,6 +930,27 @@ def ceilings(torch, steps, warmup, dev):
     _log(f"ceiling: FP6 MFMA wave + LDS-read wave per SIMD: {ovl['mfma_only']:.0f} / {ovl['lds_reads_only']:.0f} us "
          f"apart, {ovl['both']:.0f} us together ({ovl['both_over_longer']:.2f} x the longer)")
     out["mfma_lds_overlap_us"] = ovl
+
+    # LDS-DMA copies from L2 into LDS and 16-byte LDS reads per CU, apart and on four waves each
+    lib.qo_probe_lds_dma.argtypes = [c_int, c_int, c_int, c_vp, c_vp, c_vp]
+    dsrc = torch.randint(0, 255, (32 * 1024,), dtype=torch.uint8, device=dev, generator=None)
+    dma_iters = 1024
+    dma = {}
+    for mode, name, copy_waves, read_waves in ((1, "copies_only", 8, 0), (2, "reads_only", 0, 8),
+                                               (3, "four_waves_each", 4, 4)):
+        def launch(i, mode=mode):
+            assert lib.qo_probe_lds_dma(mode, cus, dma_iters, ctypes.c_void_p(dsrc.data_ptr()),
+                                        ctypes.c_void_p(fsink.data_ptr()), stream()) == 0
+        ms, _ = _time_graph(torch, launch, steps, warmup)
+        us = ms / steps * 1e3
+        # bytes per CU over the launch (both kinds end together only in the mixed mode's
+        # slower half; the per-CU rates below take the whole launch)
+        copy_b, read_b = copy_waves * dma_iters * 8 * 1024, read_waves * dma_iters * 16 * 1024
+        dma[name] = {"us_per_launch": us, "copy_GBps_per_cu": copy_b / (us * 1e-6) / 1e9,
+                     "read_GBps_per_cu": read_b / (us * 1e-6) / 1e9}
+        _log(f"ceiling: LDS {name}: {us:.0f} us, per CU {dma[name]['copy_GBps_per_cu']:.0f} GB/s copied "
+             f"from L2, {dma[name]['read_GBps_per_cu']:.0f} GB/s read")
+    out["lds_dma_per_cu"] = dma
 
     def launch_empty(i):
         assert lib.qo_probe_empty(stream()) == 0

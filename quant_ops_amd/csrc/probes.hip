@@ -16,6 +16,10 @@
 //  * qo_probe_mfma_lds_overlap: one wave per SIMD issuing FP6 MFMAs, the
 //    other issuing 16-byte LDS reads (either alone, or both), to see how far
 //    the two overlap on one SIMD (the FP6 GEMM's ping-pong relies on it);
+//  * qo_probe_lds_dma: LDS-DMA copies (global_load_lds_dwordx4, 1 KiB per
+//    instruction) from an L2-resident 32 KiB source into LDS, 16-byte LDS
+//    reads, or four waves of each per CU (the FP6 GEMM's operand path: its
+//    copies and its fragment reads share each CU's LDS);
 //  * qo_probe_empty: an empty kernel (launch and wave start-up cost);
 //  * qo_probe_stream: a streaming kernel with the quantize's traffic shape,
 //    16 bytes read and 4 bytes written per lane per step (config 2 reads
@@ -168,6 +172,42 @@ __global__ void __launch_bounds__(512) probe_mfma_lds_overlap(int mode, int iter
   out[blockIdx.x * 512 + t] = s;
 }
 
+// 512 threads. Copying waves: 8 copies of 1 KiB per iteration into the upper
+// 32 KiB of LDS (at most 16 in flight); reading waves: 16 ds_read_b128 of
+// 1 KiB per iteration from the lower 32 KiB. Mode 1: every wave copies;
+// 2: every wave reads; 3: waves 0-3 copy, waves 4-7 read. Every access lies
+// inside the 32 KiB source and the 64 KiB LDS buffer.
+__global__ void __launch_bounds__(512) probe_lds_dma(int mode, int iters, const unsigned char* __restrict__ src,
+                                                     float* out) {
+  __shared__ __align__(16) unsigned char buf[65536];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  for (int i = t; i < 16384; i += 512) reinterpret_cast<int*>(buf)[i] = i;
+  __syncthreads();
+  const bool copier = mode == 1 || (mode == 3 && wave < 4);
+  float s = 0.f;
+  if (copier) {
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)(buf + 32768);
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int c = (wave * 8 + k + it) & 31;   // source KiB; destination KiB (wave * 8 + k) % 32
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src + c * 1024 + 16 * lane),
+                     "{m0}"(base + (uint32_t)(((wave * 8 + k) & 31) * 1024))
+                     : "memory");
+      }
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    v4i acc = {0, 0, 0, 0};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc ^= *reinterpret_cast<const v4i*>(buf + ((wave * 16 + k + it) & 31) * 1024 + 16 * lane);
+    s = (float)(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]);
+  }
+  out[blockIdx.x * 512 + t] = s;
+}
+
 __global__ void probe_empty() {}
 
 // grid-stride: 16 bytes in, their four words XORed into 4 bytes out
@@ -228,6 +268,14 @@ extern "C" int qo_probe_mfma_f6_data(int kvalu, int blocks, int iters, const voi
 extern "C" int qo_probe_mfma_lds_overlap(int mode, int blocks, int iters, float* out, void* stream) {
   if (mode < 1 || mode > 3) return 1;
   probe_mfma_lds_overlap<<<blocks, 512, 0, reinterpret_cast<hipStream_t>(stream)>>>(mode, iters, out);
+  return (int)hipGetLastError();
+}
+
+// src: 32 KiB; out: blocks x 512 floats
+extern "C" int qo_probe_lds_dma(int mode, int blocks, int iters, const void* src, float* out, void* stream) {
+  if (mode < 1 || mode > 3) return 1;
+  probe_lds_dma<<<blocks, 512, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      mode, iters, static_cast<const unsigned char*>(src), out);
   return (int)hipGetLastError();
 }
 
