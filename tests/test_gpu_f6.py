@@ -6,7 +6,8 @@ them on the f8f6f4 matrix cores with block scales 2^3; its float32 sums are
 exact, so every output must equal int4_matmul_pytorch's
 (int4_matmul/ops.py:69-103) bit for bit, the same bar as the integer kernels.
 Cases: ragged M, N and K (K not a multiple of 128, K = 8), both B layouts,
-both 16-bit outputs, the three scale dtypes, bias; the full config 4 and
+both 16-bit outputs, the three scale dtypes, bias; operands and output as
+slices of wider buffers (unaligned row strides, an output pitch); the full config 4 and
 config 5 (T = 4096) products against qo_int4_gemm's integer route; the
 largest K with every product at its extreme (|sum| = 64 K); a weight
 converted once and reused; fallback and error paths; graph replay.
@@ -143,6 +144,36 @@ def test_small_workspace_falls_back_and_run_rejects(gpu):
         capi.f6_run(ws[16:], m, n, k, sa, sb)
     with pytest.raises(capi.QuantOpsError):                 # float32 outputs are not on this route
         capi.f6_run(ws, m, n, k, sa, sb, out_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("bview", [False, True])
+def test_padded_operands_and_output_pitch(gpu, bview):
+    """A, B and the output as slices of wider buffers: row strides that are
+    not multiples of four words (the conversion's word-by-word loads) and an
+    output pitch above N; bit-exact against the oracle, the padding left
+    untouched."""
+    m, n, k = 520, 300, 640
+    kp = k // 8
+    _say(f"padded operands {m}x{n}x{k} W.t()={bview}")
+    case = wl.gemm_case(m, n, k, seed=1400 + int(bview), b_transposed_view=bview, out_dtype=torch.bfloat16)
+    a_buf = torch.zeros(m, kp + 5, dtype=torch.int32)
+    a_buf[:, :kp] = case.a
+    a = a_buf.to(gpu)[:, :kp]
+    if bview:
+        w_buf = torch.zeros(n, kp + 3, dtype=torch.int32)
+        w_buf[:, :kp] = case.b.t()
+        b = w_buf.to(gpu)[:, :kp].t()
+    else:
+        b_buf = torch.zeros(kp, n + 7, dtype=torch.int32)
+        b_buf[:, :n] = case.b
+        b = b_buf.to(gpu)[:, :n]
+    out_buf = torch.full((m, n + 9), 7.0, dtype=torch.bfloat16, device=gpu)
+    out = out_buf[:, :n]
+    capi.int4_gemm(a, b, case.scale_a.to(gpu), case.scale_b.to(gpu), out_dtype=torch.bfloat16, out=out,
+                   workspace=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), _ref(case, case.scale_a, case.scale_b, torch.bfloat16))
+    assert bool((out_buf[:, n:] == 7.0).all())
 
 
 def test_route_switch(gpu, routing):
