@@ -1,0 +1,79 @@
+"""Codes at rounding ties, bit-exact: with permutation matrices as L and R
+(orthogonal, each product a single term times 1.0) the transformed Y is an
+exact permutation of X, so every rounding the kernels do before the codes is
+exact and their codes and scales must equal the oracle's
+(flatquant/ops.py:78-130) bit for bit, with no flip budget.
+
+Each token holds one element of magnitude 7 (its absmax, so at clip 1.0 the
+bf16 scale is exactly 1 and each quotient is the element itself) and draws
+the rest from the values the code step must get right: every half-integer
+tie in [-7, 7] (round half to even), their bf16 neighbours on both sides,
+integers, zeros of both signs and tiny values. At clip 0.9 the same tokens
+take the clamped code form (quotients up to 7 / 0.9), at clip 1.0 the
+unclamped one; the 64 x 64 shape runs the one-wave kernel, 112 x 128 and
+64 x 128 the few-token kernel (packed and int8 codes), at 300 tokens (one
+per workgroup) and 1200 (several per workgroup: the staged code copies).
+"""
+import pytest
+import torch
+
+from quant_ops_amd import capi
+from oracle import fq_reference as ofq
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[gpu-codes-exact] {msg}", flush=True)
+
+
+def _tie_values():
+    """bf16 values in [-7, 7] around every rounding decision of the code step."""
+    vals = []
+    for k in range(-7, 7):
+        h = torch.tensor(k + 0.5, dtype=torch.bfloat16)
+        bits = h.view(torch.int16)
+        up = (bits + 1).view(torch.bfloat16) if float(h) > 0 else (bits - 1).view(torch.bfloat16)
+        down = (bits - 1).view(torch.bfloat16) if float(h) > 0 else (bits + 1).view(torch.bfloat16)
+        vals += [float(h), float(up), float(down), float(k)]
+    vals += [0.0, -0.0, 7.0, -7.0, 1e-30, -1e-30, 6.96875, -6.96875]
+    return torch.tensor(vals, dtype=torch.float32)
+
+
+def _permutation(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    p = torch.randperm(n, generator=g)
+    return torch.eye(n)[p]
+
+
+def _tokens(tokens, m, n, seed):
+    g = torch.Generator().manual_seed(seed)
+    vals = _tie_values()
+    idx = torch.randint(0, vals.numel(), (tokens, m * n), generator=g)
+    x = vals[idx]
+    # one element of magnitude 7 per token (either sign) fixes its absmax
+    pos = torch.randint(0, m * n, (tokens,), generator=g)
+    sign = torch.where(torch.rand(tokens, generator=g) < 0.5, -7.0, 7.0)
+    x[torch.arange(tokens), pos] = sign
+    x[tokens // 2].zero_()                      # an all-zero token (scale at its floor)
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("m,n,tokens,clip,pack", [
+    (112, 128, 300, 1.0, True), (112, 128, 1200, 1.0, True), (112, 128, 300, 0.9, True),
+    (112, 128, 1200, 0.9, True), (112, 128, 300, 0.9, False), (64, 128, 600, 1.0, True),
+    (64, 128, 600, 0.9, True), (64, 64, 500, 1.0, True), (64, 64, 500, 0.9, True),
+])
+def test_codes_at_ties_bit_exact(gpu, m, n, tokens, clip, pack):
+    _say(f"{tokens} x {m}x{n} bf16 clip={clip} pack={pack}")
+    x = _tokens(tokens, m, n, seed=31 * m + n + tokens)
+    left = _permutation(m, seed=m).to(torch.bfloat16)
+    right = _permutation(n, seed=n + 1).to(torch.bfloat16)
+    q, s = capi.flatquant_quantize(x.to(gpu), left.to(gpu), right.to(gpu), clip, pack)
+    torch.cuda.synchronize()
+    q_ref, s_ref = ofq.flatquant_pytorch(x, left, right, clip, pack)
+    assert torch.equal(s.cpu(), s_ref.float()), "scales"
+    if pack:
+        assert torch.equal(q.cpu(), q_ref), "packed codes"
+    else:
+        assert torch.equal(q.cpu(), q_ref.to(q.dtype)), "int8 codes"
