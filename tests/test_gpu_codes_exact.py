@@ -9,10 +9,11 @@ bf16 scale is exactly 1 and each quotient is the element itself) and draws
 the rest from the values the code step must get right: every half-integer
 tie in [-7, 7] (round half to even), their bf16 neighbours on both sides,
 integers, zeros of both signs and tiny values. At clip 0.9 the same tokens
-take the clamped code form (quotients up to 7 / 0.9), at clip 1.0 the
-unclamped one; the 64 x 64 shape runs the one-wave kernel, 112 x 128 and
-64 x 128 the few-token kernel (packed and int8 codes), at 300 tokens (one
-per workgroup) and 1200 (several per workgroup: the staged code copies).
+take the clamped bf16 code form (quotients up to 7 / 0.9), at clip 1.0 the
+unclamped one; fp16 tokens at clip 1.0 take the fp16 form. The 64 x 64
+shape runs the one-wave kernel, 112 x 128 and 64 x 128 the few-token kernel
+(packed and int8 codes), at 300 tokens (one per workgroup) and 1200 (several
+per workgroup: the staged code copies).
 """
 import pytest
 import torch
@@ -27,16 +28,17 @@ def _say(msg):
     print(f"[gpu-codes-exact] {msg}", flush=True)
 
 
-def _tie_values():
-    """bf16 values in [-7, 7] around every rounding decision of the code step."""
+def _tie_values(dtype):
+    """Values of ``dtype`` in [-7, 7] around every rounding decision of the code step."""
     vals = []
     for k in range(-7, 7):
-        h = torch.tensor(k + 0.5, dtype=torch.bfloat16)
+        h = torch.tensor(k + 0.5, dtype=dtype)
         bits = h.view(torch.int16)
-        up = (bits + 1).view(torch.bfloat16) if float(h) > 0 else (bits - 1).view(torch.bfloat16)
-        down = (bits - 1).view(torch.bfloat16) if float(h) > 0 else (bits + 1).view(torch.bfloat16)
+        up = (bits + 1).view(dtype) if float(h) > 0 else (bits - 1).view(dtype)
+        down = (bits - 1).view(dtype) if float(h) > 0 else (bits + 1).view(dtype)
         vals += [float(h), float(up), float(down), float(k)]
-    vals += [0.0, -0.0, 7.0, -7.0, 1e-30, -1e-30, 6.96875, -6.96875]
+    tiny = 1e-30 if dtype == torch.bfloat16 else 1e-7
+    vals += [0.0, -0.0, 7.0, -7.0, tiny, -tiny, 6.96875, -6.96875]
     return torch.tensor(vals, dtype=torch.float32)
 
 
@@ -46,17 +48,18 @@ def _permutation(n, seed):
     return torch.eye(n)[p]
 
 
-def _tokens(tokens, m, n, seed):
+def _tokens(tokens, m, n, seed, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
-    vals = _tie_values()
+    vals = _tie_values(dtype)
     idx = torch.randint(0, vals.numel(), (tokens, m * n), generator=g)
     x = vals[idx]
     # one element of magnitude 7 per token (either sign) fixes its absmax
     pos = torch.randint(0, m * n, (tokens,), generator=g)
     sign = torch.where(torch.rand(tokens, generator=g) < 0.5, -7.0, 7.0)
     x[torch.arange(tokens), pos] = sign
-    x[tokens // 2].zero_()                      # an all-zero token (scale at its floor)
-    return x.to(torch.bfloat16)
+    if dtype == torch.bfloat16:
+        x[tokens // 2].zero_()                  # an all-zero token (scale at its floor)
+    return x.to(dtype)
 
 
 @pytest.mark.parametrize("m,n,tokens,clip,pack", [
@@ -77,3 +80,20 @@ def test_codes_at_ties_bit_exact(gpu, m, n, tokens, clip, pack):
         assert torch.equal(q.cpu(), q_ref), "packed codes"
     else:
         assert torch.equal(q.cpu(), q_ref.to(q.dtype)), "int8 codes"
+
+
+@pytest.mark.parametrize("m,n,tokens", [(64, 64, 2048), (112, 128, 300), (64, 128, 600)])
+def test_fp16_codes_at_ties_bit_exact(gpu, m, n, tokens):
+    """The fp16 code form (a packed add of 1536 + 8 rounds each quotient) at
+    clip 1.0, where the fp16 scale of an absmax of 7 is exactly 1; config 2's
+    shape and token count first. (The all-zero token is left out: its fp16
+    scale floor rounds to 0, a case the other tests cover.)"""
+    _say(f"{tokens} x {m}x{n} fp16 clip=1.0")
+    x = _tokens(tokens, m, n, seed=17 * m + n + tokens, dtype=torch.float16)
+    left = _permutation(m, seed=m + 5).to(torch.float16)
+    right = _permutation(n, seed=n + 6).to(torch.float16)
+    q, s = capi.flatquant_quantize(x.to(gpu), left.to(gpu), right.to(gpu), 1.0, True)
+    torch.cuda.synchronize()
+    q_ref, s_ref = ofq.flatquant_pytorch(x, left, right, 1.0, True)
+    assert torch.equal(s.cpu(), s_ref.float()), "scales"
+    assert torch.equal(q.cpu(), q_ref), "packed codes"
