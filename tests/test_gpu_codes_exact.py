@@ -33,11 +33,11 @@ def _tie_values(dtype):
     vals = []
     for k in range(-7, 7):
         h = torch.tensor(k + 0.5, dtype=dtype)
-        bits = h.view(torch.int16)
+        bits = h.view(torch.int32 if dtype == torch.float32 else torch.int16)
         up = (bits + 1).view(dtype) if float(h) > 0 else (bits - 1).view(dtype)
         down = (bits - 1).view(dtype) if float(h) > 0 else (bits + 1).view(dtype)
         vals += [float(h), float(up), float(down), float(k)]
-    tiny = 1e-30 if dtype == torch.bfloat16 else 1e-7
+    tiny = 1e-7 if dtype == torch.float16 else 1e-30
     vals += [0.0, -0.0, 7.0, -7.0, tiny, -tiny, 6.96875, -6.96875]
     return torch.tensor(vals, dtype=torch.float32)
 
@@ -97,3 +97,16 @@ def test_fp16_codes_at_ties_bit_exact(gpu, m, n, tokens):
     q_ref, s_ref = ofq.flatquant_pytorch(x, left, right, 1.0, True)
     assert torch.equal(s.cpu(), s_ref.float()), "scales"
     assert torch.equal(q.cpu(), q_ref), "packed codes"
+
+
+def test_fp32_int8_codes_at_ties_bit_exact(gpu):
+    """fp32 inputs with int8 codes (config 1's dtype, layout and shape), clip 1.0."""
+    m, n, tokens = 64, 64, 128
+    _say(f"{tokens} x {m}x{n} fp32 clip=1.0 int8 codes")
+    x = _tokens(tokens, m, n, seed=77, dtype=torch.float32)
+    left, right = _permutation(m, seed=3), _permutation(n, seed=4)
+    q, s = capi.flatquant_quantize(x.to(gpu), left.to(gpu), right.to(gpu), 1.0, False)
+    torch.cuda.synchronize()
+    q_ref, s_ref = ofq.flatquant_pytorch(x, left, right, 1.0, False)
+    assert torch.equal(s.cpu(), s_ref.float()), "scales"
+    assert torch.equal(q.cpu(), q_ref.to(q.dtype)), "int8 codes"
